@@ -1,0 +1,179 @@
+#!/usr/bin/env python3
+"""Benchmark of the causal attention forward on one MI355X.
+
+Workload (BASELINE.json metric and configs[2]): causal attention forward, bf16, d=64, at
+the GPT-2-XL shape B=8, H=25, N=1024; Q, K ~ N(0, 3^2), V ~ N(0, 1); scale 1/8.  One step =
+one launch of the kernel over one batch (O and LSE written).  Inputs are synthetic and
+already resident in HBM; four input sets are rotated so the 105 MB working set of one
+call does not stay in the 256 MB Infinity Cache from one step to the next.
+
+Prints one JSON line.  ``value`` is TFLOP/s with the FlashAttention causal convention
+(4*B*H*N^2*d/2 FLOPs per forward).  ``roofline`` compares it with the dense bf16 MFMA peak;
+``cpu_baseline`` times the reference's PyTorch CPU attention path (the "manual" branch of
+src/py/model_inference.py:68-75) on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tfg-flashattention_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "causal attn fwd TFLOP/s bf16 d=64 @ GPT-2-XL shape; % of bf16 MFMA peak"
+B, H, N, D = 8, 25, 1024, 64
+SIGMA_QK, SIGMA_V = 3.0, 1.0
+SCALE = 1.0 / math.sqrt(D)
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published)
+PEAK_HBM_GBS = 8000.0
+N_SETS = 4
+
+
+def flops_per_fwd(b=B, h=H, n=N, d=D):
+    return 4.0 * b * h * n * n * d / 2.0
+
+
+def bytes_per_fwd(b=B, h=H, n=N, d=D):
+    return 2.0 * 4 * b * h * n * d + 4.0 * b * h * n
+
+
+def cpu_baseline(gpu_o_sample, q_sample, k_sample, v_sample, heads_in_sample):
+    """Times the reference's PyTorch CPU "manual" attention (fp32) on a sample of the
+    workload: the first `heads_in_sample` (b, h) heads of input set 0, full N.  Reports
+    TFLOP/s with the same algorithmic FLOP count (the manual path itself computes the full
+    N x N matrix, twice that)."""
+    import torch
+
+    from oracle import manual_attention_torch
+
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(cores)
+    q, k, v = q_sample.float().cpu(), k_sample.float().cpu(), v_sample.float().cpu()
+    manual_attention_torch(q[:, :1], k[:, :1], v[:, :1])  # warm-up
+    times = []
+    out = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        out = manual_attention_torch(q, k, v)
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    fl = flops_per_fwd(1, heads_in_sample, N, D)
+    max_err = (out - gpu_o_sample.float().cpu()).abs().max().item()
+    return {
+        "value": fl / sec / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{heads_in_sample} of {B * H} heads (B=1 x H={heads_in_sample}, N={N}, d={D}) of "
+                   f"the bench inputs, torch {torch.__version__} fp32 manual path, median of 3 runs "
+                   f"= {sec:.3f} s; same algorithmic FLOPs per head as the GPU figure"),
+        "seconds_per_sample": sec,
+        "max_abs_diff_vs_gpu": max_err,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=25,
+                    help="heads of the workload timed by the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards over (batch, head) with no exchange; one GPU's share is what "
+              "is measured)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import custom_flash_attn
+    from custom_flash_attn import _C
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    info = custom_flash_attn.device_info()
+
+    gen = torch.Generator(device=dev).manual_seed(1003)
+    sets = []
+    for _ in range(N_SETS):
+        q = (torch.randn(B, H, N, D, device=dev, generator=gen) * SIGMA_QK).to(torch.bfloat16)
+        k = (torch.randn(B, H, N, D, device=dev, generator=gen) * SIGMA_QK).to(torch.bfloat16)
+        v = (torch.randn(B, H, N, D, device=dev, generator=gen) * SIGMA_V).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        lse = torch.empty(B, H, N, device=dev, dtype=torch.float32)
+        sets.append((q, k, v, o, lse))
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def step(i):
+        q, k, v, o, lse = sets[i % N_SETS]
+        _C.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+               B, H, N, D, SCALE, True, sh)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(args.steps):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+
+    tflops = flops_per_fwd() / (ms * 1e-3) / 1e12
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "config3: causal attention forward, GPT-2-XL shape, Q,K~N(0,3^2) V~N(0,1), O + LSE",
+            "B": B, "H": H, "N": N, "d": D, "causal": True, "scale": SCALE,
+            "input_sets_rotated": N_SETS,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_bytes": bytes_per_fwd(),
+            "hbm_GBps_at_algorithmic_bytes": round(bytes_per_fwd() / (ms * 1e-3) / 1e9, 1),
+            "hbm_ceiling_frac_of_mfma_peak": round(
+                min(1.0, flops_per_fwd() / bytes_per_fwd() * PEAK_HBM_GBS * 1e9 / (PEAK_BF16_TFLOPS * 1e12)), 4),
+        },
+        "device": info,
+    }
+    if not args.no_cpu_baseline:
+        nh = max(1, min(args.cpu_heads, H))
+        q, k, v, o, _ = sets[0]
+        torch.cuda.synchronize()
+        result["cpu_baseline"] = cpu_baseline(o[:1, :nh], q[:1, :nh], k[:1, :nh], v[:1, :nh], nh)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

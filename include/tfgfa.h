@@ -1,0 +1,90 @@
+/*
+ * tfgfa.h - C ABI of the MI355X (gfx950) causal FlashAttention forward.
+ *
+ * This is the drop-in boundary for the reference's single hot path:
+ *
+ *   custom_flash_attn.forward(Q, K_mat, V) -> O
+ *     reference: src/cpp/torch_bind.cpp:21-49 (pybind11/libtorch binding)
+ *             -> src/cpp/v1.cu:4-38 (host launcher flashattention_forward<T>)
+ *             -> src/cpp/headers/v1_implementation.hpp:12-171 (device kernel)
+ *
+ * The reference binds the launcher through a C++ template declaration
+ * (torch_bind.cpp:9-11); here the same step is a plain C function taking
+ * device pointers, sizes and a HIP stream, with no torch types, so that any
+ * FFI (pybind11, ctypes, cgo ...) can bind it.
+ *
+ * Conventions shared by every entry point:
+ *  - Q, K, V, O are contiguous (B, H, N, D) bfloat16 tensors in device memory
+ *    (strides H*N*D, N*D, D, 1), 16-byte aligned.  This is the layout
+ *    torch_bind.cpp:27-31 assumes (size(0..2) read as B, H, N; O = empty_like(Q)).
+ *  - LSE, when requested, is a contiguous (B, H, N) float32 tensor holding the
+ *    natural-log log-sum-exp of each row's scaled, masked scores:
+ *        LSE[b,h,i] = log( sum_{j <= i} exp(scale * q_i . k_j) )
+ *    (the lse_i of src/py/triton_implementation.py:153-154, which the
+ *    reference computes but never stores, :162-166).
+ *  - The caller owns every buffer; the library allocates no device memory.
+ *  - Return value: 0 on success, > 0 invalid argument (checked before any HIP
+ *    call, so argument errors are reported identically with or without a GPU),
+ *    < 0 the negated hipError_t of a failed HIP call.
+ *  - Calls are reentrant; launches are asynchronous on the given stream.
+ */
+#ifndef TFGFA_H
+#define TFGFA_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TFGFA_ABI_VERSION 1
+
+/* Status codes (> 0: invalid argument). */
+#define TFGFA_OK                 0
+#define TFGFA_ERR_NULL_POINTER   1  /* q, k, v or o is NULL                          */
+#define TFGFA_ERR_BAD_SHAPE      2  /* B, H or N negative                            */
+#define TFGFA_ERR_HEAD_DIM       3  /* D is not a compiled head dimension (only 64)  */
+#define TFGFA_ERR_SCALE          4  /* softmax_scale not finite or not > 0           */
+#define TFGFA_ERR_CAUSAL_FLAG    5  /* causal is neither 0 nor 1                     */
+#define TFGFA_ERR_TOO_LARGE      6  /* grid or element count exceeds the limits      */
+#define TFGFA_ERR_ALIGNMENT      7  /* q/k/v/o not 16-byte aligned or lse not 4-byte */
+
+/*
+ * Attention forward, bf16 in / bf16 out, fp32 accumulation and softmax.
+ *
+ *   O[b,h,i,:] = sum_j softmax_j(scale * Q[b,h,i,:] . K[b,h,j,:]) * V[b,h,j,:]
+ *   with j <= i when causal == 1 (top-left aligned, diagonal included), all j otherwise.
+ *
+ * Replaces flashattention_forward<__nv_bfloat16>(O, Q, K_mat, V, seq_len,
+ * batch_size, num_heads) (src/cpp/v1.cu:4-38, instantiated :40-42), whose
+ * scale is fixed to 1/sqrt(64) (v1.cu:16) and whose launch goes to the legacy
+ * default stream (v1.cu:33-34).  Here the scale is explicit (pass 0.125 for
+ * the reference's behaviour), `lse` may be NULL, and `hip_stream` (a
+ * hipStream_t, NULL = default stream) is the stream the caller is using.
+ * B, H or N equal to 0 is an empty problem: nothing is launched, 0 returned.
+ */
+int tfgfa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
+                   int B, int H, int N, int D, float softmax_scale, int causal,
+                   void* hip_stream);
+
+/*
+ * Human-readable text for a status code returned by any tfgfa_* function.
+ * The string is static.  Replaces the TORCH_CHECK messages of
+ * src/cpp/torch_bind.cpp:13-19, :41 for errors detected below the binding
+ * (the reference drops launcher errors, torch_bind.cpp:34-39).
+ */
+const char* tfgfa_strerror(int status);
+
+/*
+ * Properties of the current HIP device, queried once per device and cached
+ * (the reference queries device 0 on every call, v1.cu:7-8).  Any output
+ * pointer may be NULL.  `arch` receives the gcnArchName (e.g. "gfx950:sramecc+:xnack-").
+ */
+int tfgfa_device_info(int* cu_count, int* sclk_mhz, char* arch, int arch_len);
+
+/* ABI version of the loaded library (TFGFA_ABI_VERSION at build time). */
+int tfgfa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TFGFA_H */

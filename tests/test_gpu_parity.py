@@ -1,0 +1,252 @@
+"""Parity of the HIP kernel with the CPU oracle (GPU box only).
+
+Tolerances: against the fp64/fp32 oracle on the same
+bf16-rounded inputs, max|dO| <= 2e-2 and mean|dO| <= 2e-3; LSE (natural log) max
+abs error <= 1e-3.  Shapes: BASELINE.json configs 1-4 (config 1 and 2 in full,
+config 3 and 4 on sampled query rows of every head), the reference's boundary
+lengths (test/py/test_cuda_implementation.py:93) and more edge cases.
+
+Every call goes through the C ABI (via custom_flash_attn / _C).
+"""
+import json
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import CONFIGS, attention_c, bf16_bits_to_f32, make_inputs, sha256_bf16
+
+import custom_flash_attn
+from custom_flash_attn import _C
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL_MAX, TOL_MEAN, TOL_LSE = 2e-2, 2e-3, 1e-3
+DEV = "cuda:0"
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _to_dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(torch.bfloat16).to(DEV)
+
+
+def _run(q, k, v, scale=None, causal=True):
+    """numpy float32 (bf16-valued) inputs -> (O float32 numpy, LSE numpy)."""
+    qd, kd, vd = _to_dev(q), _to_dev(k), _to_dev(v)
+    o, lse = custom_flash_attn.forward_lse(qd, kd, vd, softmax_scale=scale, causal=causal)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), lse.cpu().numpy()
+
+
+def _check(o, lse, o_ref, lse_ref, label):
+    d = np.abs(o.astype(np.float64) - o_ref)
+    dl = np.abs(lse.astype(np.float64) - lse_ref)
+    _say(f"{label}: max|dO|={d.max():.3e} mean|dO|={d.mean():.3e} max|dLSE|={dl.max():.3e}")
+    assert np.isfinite(o).all() and np.isfinite(lse).all(), f"{label}: non-finite output"
+    assert d.max() <= TOL_MAX, f"{label}: max|dO| {d.max()}"
+    assert d.mean() <= TOL_MEAN, f"{label}: mean|dO| {d.mean()}"
+    assert dl.max() <= TOL_LSE, f"{label}: max|dLSE| {dl.max()}"
+
+
+def _rand(shape, seed, sigma=1.0):
+    g = np.random.Generator(np.random.PCG64(seed))
+    return (g.standard_normal(shape, dtype=np.float32) * np.float32(sigma))
+
+
+def _bf(x):
+    return torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+
+
+# ------------------------------------------------------------------ fixtures
+
+
+GOLDEN_FILES = sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz"))
+
+
+@pytest.mark.parametrize("fname", GOLDEN_FILES)
+def test_golden_fixtures(fname):
+    z = np.load(os.path.join(GOLDEN, fname))
+    q, k, v = (bf16_bits_to_f32(z[n]) for n in ("q_bits", "k_bits", "v_bits"))
+    _say(f"golden {fname} shape={q.shape}")
+    o, lse = _run(q, k, v, float(z["scale"]), bool(z["causal"]))
+    _check(o, lse, z["o"], z["lse"], fname)
+
+
+# ------------------------------------------------------------------ BASELINE configs
+
+
+def _config_inputs(name):
+    cfg = CONFIGS[name]
+    q, k, v = make_inputs(cfg)
+    with open(os.path.join(GOLDEN, "inputs_sha256.json")) as f:
+        want = json.load(f)[name]
+    assert (sha256_bf16(q), sha256_bf16(k), sha256_bf16(v)) == (want["q"], want["k"], want["v"])
+    return cfg, q, k, v
+
+
+@pytest.mark.parametrize("name", ["config1", "config2"])
+def test_config_full(name):
+    cfg, q, k, v = _config_inputs(name)
+    _say(f"{name} B={cfg.B} H={cfg.H} N={cfg.N}")
+    o, lse = _run(q, k, v, cfg.scale, True)
+    o_ref, lse_ref = attention_c(q, k, v, cfg.scale, True)
+    _check(o, lse, o_ref, lse_ref, name)
+
+
+@pytest.mark.parametrize("name,nsample", [("config3", 96), ("config4", 40)])
+def test_config_sampled_rows(name, nsample):
+    cfg, q, k, v = _config_inputs(name)
+    _say(f"{name} B={cfg.B} H={cfg.H} N={cfg.N} (sampled rows)")
+    o, lse = _run(q, k, v, cfg.scale, True)
+    g = np.random.Generator(np.random.PCG64(7))
+    edges = [0, 1, 31, 32, 63, 64, 127, 128, 129, cfg.N // 2, cfg.N - 2, cfg.N - 1]
+    rows = np.unique(np.concatenate([edges, g.integers(0, cfg.N, nsample - len(edges))]))
+    o_ref, lse_ref = attention_c(q, k, v, cfg.scale, True, rows=rows)
+    _check(o[:, :, rows], lse[:, :, rows], o_ref, lse_ref, name)
+    # Whole-tensor properties at full size.
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
+    np.testing.assert_array_equal(o[:, :, 0], v[:, :, 0])  # row 0 attends only to key 0
+    assert np.all(np.abs(o) <= np.abs(v).max() + 1e-2)    # convex combination of V rows
+
+
+# ------------------------------------------------------------------ reference test shapes
+
+
+@pytest.mark.parametrize("T", [1, 2, 10, 11, 15, 33, 63, 64, 65, 127, 128, 129, 255, 257, 1000, 1024])
+def test_boundary_lengths(T):
+    """The reference's boundary lengths (test_cuda_implementation.py:93) and tile edges."""
+    q, k, v = (_bf(_rand((2, 4, T, 64), 1000 + 3 * T + i)) for i in range(3))
+    _say(f"boundary T={T}")
+    o, lse = _run(q, k, v)
+    o_ref, lse_ref = attention_c(q, k, v, 0.125, True)
+    _check(o, lse, o_ref, lse_ref, f"T={T}")
+
+
+@pytest.mark.parametrize("T", [1, 33, 64, 100, 128, 300, 1024])
+def test_non_causal(T):
+    q, k, v = (_bf(_rand((1, 3, T, 64), 2000 + T + i)) for i in range(3))
+    _say(f"non-causal T={T}")
+    o, lse = _run(q, k, v, 0.125, False)
+    o_ref, lse_ref = attention_c(q, k, v, 0.125, False)
+    _check(o, lse, o_ref, lse_ref, f"noncausal T={T}")
+
+
+@pytest.mark.parametrize("scale", [0.05, 0.3, 1.0])
+def test_explicit_scale(scale):
+    q, k, v = (_bf(_rand((1, 2, 200, 64), 3000 + i)) for i in range(3))
+    o, lse = _run(q, k, v, scale, True)
+    o_ref, lse_ref = attention_c(q, k, v, scale, True)
+    _check(o, lse, o_ref, lse_ref, f"scale={scale}")
+
+
+def test_matches_reference_test_vs_sdpa_fp32():
+    """test_flash_attention_vs_pytorch (test_cuda_implementation.py:72-91), against SDPA in fp32."""
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(2, 4, 128, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    out = custom_flash_attn.forward(q, k, v)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True)
+    torch.testing.assert_close(out.float(), ref, rtol=1e-2, atol=1e-2)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16 and out.device == q.device
+
+
+# ------------------------------------------------------------------ invariants / sanitizing
+
+
+def test_outputs_fully_written_and_guards_untouched():
+    """NaN-poisoned outputs inside guard canaries: every element written, nothing outside."""
+    B, H, N = 2, 3, 300
+    q, k, v = (torch.randn(B, H, N, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    guard = 4096
+    o_buf = torch.full((guard + B * H * N * 64 + guard,), float("nan"), device=DEV, dtype=torch.bfloat16)
+    l_buf = torch.full((guard + B * H * N + guard,), float("nan"), device=DEV, dtype=torch.float32)
+    o_buf[:guard] = 7.0
+    o_buf[-guard:] = 7.0
+    l_buf[:guard] = 7.0
+    l_buf[-guard:] = 7.0
+    o = o_buf[guard:-guard]
+    lse = l_buf[guard:-guard]
+    _C.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), B, H, N, 64,
+           0.125, True, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all()
+    assert (o_buf[:guard] == 7.0).all() and (o_buf[-guard:] == 7.0).all()
+    assert (l_buf[:guard] == 7.0).all() and (l_buf[-guard:] == 7.0).all()
+
+
+def test_deterministic_bitwise():
+    q, k, v = (torch.randn(4, 8, 777, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    o1, l1 = custom_flash_attn.forward_lse(q, k, v)
+    o2, l2 = custom_flash_attn.forward_lse(q, k, v)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def test_causality_bitwise():
+    q, k, v = (torch.randn(2, 4, 512, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    o1 = custom_flash_attn.forward(q, k, v)
+    i = 200
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :, i + 1:] = torch.randn_like(k2[:, :, i + 1:])
+    v2[:, :, i + 1:] = torch.randn_like(v2[:, :, i + 1:])
+    o2 = custom_flash_attn.forward(q, k2, v2)
+    assert torch.equal(o1[:, :, : i + 1], o2[:, :, : i + 1])
+    assert not torch.equal(o1[:, :, i + 1:], o2[:, :, i + 1:])
+
+
+def test_identical_keys_prefix_mean_and_constant_v():
+    B, H, N = 1, 4, 300
+    q = torch.randn(B, H, N, 64, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(B, H, 1, 64, device=DEV, dtype=torch.bfloat16).expand(B, H, N, 64).contiguous()
+    v = torch.randn(B, H, N, 64, device=DEV, dtype=torch.bfloat16)
+    o, lse = custom_flash_attn.forward_lse(q, k, v)
+    mean = torch.cumsum(v.double(), dim=2) / torch.arange(1, N + 1, device=DEV, dtype=torch.float64)[None, None, :, None]
+    assert (o.double() - mean).abs().max().item() <= TOL_MAX
+    s = 0.125 * (q.double() * k.double()).sum(-1)
+    ln = torch.log(torch.arange(1, N + 1, device=DEV, dtype=torch.float64))
+    assert (lse.double() - (s + ln)).abs().max().item() <= TOL_LSE
+    ones = torch.ones_like(v)
+    o1 = custom_flash_attn.forward(q * 3, torch.randn_like(q) * 3, ones)
+    assert (o1.float() - 1).abs().max().item() <= 1e-2
+
+
+def test_empty_inputs():
+    for shape in [(0, 2, 16, 64), (2, 0, 16, 64), (2, 2, 0, 64)]:
+        q = torch.empty(shape, device=DEV, dtype=torch.bfloat16)
+        o = custom_flash_attn.forward(q, q, q)
+        assert o.shape == q.shape
+
+
+def test_error_paths_on_device():
+    q = torch.randn(1, 2, 16, 64, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="^K_mat must be contiguous$"):
+        custom_flash_attn.forward(q, q.transpose(2, 3).contiguous().transpose(2, 3), q)
+    with pytest.raises(RuntimeError, match="Use bfloat16"):
+        custom_flash_attn.forward(q.half(), q.half(), q.half())
+    with pytest.raises(RuntimeError, match="head_dim must be 64"):
+        x = torch.randn(1, 2, 16, 128, device=DEV, dtype=torch.bfloat16)
+        custom_flash_attn.forward(x, x, x)
+
+
+def test_runs_on_side_stream():
+    q, k, v = (torch.randn(2, 4, 300, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    ref = custom_flash_attn.forward(q, k, v)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        out = custom_flash_attn.forward(q, k, v)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+def test_device_info():
+    info = custom_flash_attn.device_info()
+    _say(f"device_info: {info}")
+    assert info["cu_count"] > 0 and info["sclk_mhz"] > 0 and info["arch"].startswith("gfx")

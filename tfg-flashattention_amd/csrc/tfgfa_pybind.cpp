@@ -1,0 +1,62 @@
+// tfgfa_pybind.cpp - pybind11 module `custom_flash_attn._C`, a thin layer over the C ABI.
+//
+// Plays the role of the reference's PYBIND11_MODULE (src/cpp/torch_bind.cpp:47-49), but it
+// does not depend on libtorch: it takes raw device pointers, sizes and a stream handle.  The
+// Python package (custom_flash_attn/__init__.py) does the tensor checks and allocation that
+// torch_bind.cpp:13-31 does in C++.  The GIL is released around the launch, and a non-zero
+// C-ABI status becomes a Python RuntimeError (the reference drops launcher errors,
+// torch_bind.cpp:34-39).
+#include <pybind11/pybind11.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "tfgfa.h"
+
+namespace py = pybind11;
+
+namespace {
+
+void fwd(std::uintptr_t q, std::uintptr_t k, std::uintptr_t v, std::uintptr_t o, std::uintptr_t lse,
+         int B, int H, int N, int D, float softmax_scale, bool causal, std::uintptr_t stream) {
+  int st;
+  {
+    py::gil_scoped_release nogil;
+    st = tfgfa_fwd_bf16(reinterpret_cast<const void*>(q), reinterpret_cast<const void*>(k),
+                        reinterpret_cast<const void*>(v), reinterpret_cast<void*>(o),
+                        reinterpret_cast<float*>(lse), B, H, N, D, softmax_scale, causal ? 1 : 0,
+                        reinterpret_cast<void*>(stream));
+  }
+  if (st != TFGFA_OK) {
+    throw std::runtime_error(std::string("tfgfa_fwd_bf16 failed (status ") + std::to_string(st) +
+                             "): " + tfgfa_strerror(st));
+  }
+}
+
+py::dict device_info() {
+  int cu = 0, mhz = 0;
+  char arch[128] = {0};
+  const int st = tfgfa_device_info(&cu, &mhz, arch, sizeof(arch));
+  if (st != TFGFA_OK) {
+    throw std::runtime_error(std::string("tfgfa_device_info failed: ") + tfgfa_strerror(st));
+  }
+  py::dict d;
+  d["cu_count"] = cu;
+  d["sclk_mhz"] = mhz;
+  d["arch"] = std::string(arch);
+  return d;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_C, m) {
+  m.doc() = "MI355X causal FlashAttention forward (C-ABI binding)";
+  m.def("fwd", &fwd, "Launch the bf16 attention forward on raw device pointers", py::arg("q"),
+        py::arg("k"), py::arg("v"), py::arg("o"), py::arg("lse"), py::arg("B"), py::arg("H"),
+        py::arg("N"), py::arg("D"), py::arg("softmax_scale"), py::arg("causal"),
+        py::arg("stream"));
+  m.def("device_info", &device_info, "CU count, shader clock (MHz) and arch of the current device");
+  m.def("strerror", [](int st) { return std::string(tfgfa_strerror(st)); });
+  m.def("abi_version", []() { return tfgfa_abi_version(); });
+}

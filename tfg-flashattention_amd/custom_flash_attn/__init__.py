@@ -1,0 +1,118 @@
+"""custom_flash_attn - MI355X (gfx950) causal FlashAttention forward.
+
+Drop-in for the reference's extension module of the same name
+(src/cpp/torch_bind.cpp:21-49, built by src/py/setup.py:7-26), which the GPT-2
+attention module calls as ``custom_flash_attn.forward(q, k, v)``
+(src/py/model_inference.py:85-90).
+
+The module layout differs from the reference on purpose: the compute lives in
+``libtfgfa.so`` (hand-written HIP for gfx950 behind the C ABI of
+``include/tfgfa.h``) and ``_C`` is a pybind11 binding over that ABI with no
+libtorch in it.  This file does what torch_bind.cpp:13-31 does in C++: check
+the tensors, allocate O with ``torch.empty_like`` and launch on the caller's
+current stream.  There is no CPU or PyTorch fallback: if the native library is
+missing, importing this package raises.
+"""
+from __future__ import annotations
+
+import math
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+
+try:
+    from . import _C  # noqa: F401  (loads libtfgfa.so through its rpath)
+except ImportError as exc:  # pragma: no cover - exercised only on a broken build
+    raise ImportError(
+        "custom_flash_attn: native extension not built "
+        f"({exc}); run `make -C tfg-flashattention_amd/csrc` or __graft_entry__.build()"
+    ) from exc
+
+__all__ = ["forward", "forward_lse", "device_info", "HEAD_DIM", "library_path"]
+
+HEAD_DIM = 64  # the only compiled head dimension (common_types.hpp:33 fixes K = 64 too)
+
+
+def library_path() -> str:
+    """Absolute path of the HIP shared library this package launches."""
+    return os.path.join(_HERE, "libtfgfa.so")
+
+
+def _check_input(x: torch.Tensor, name: str) -> None:
+    # Same order and text as CHECK_CUDA / CHECK_CONTIGUOUS (torch_bind.cpp:13-19).
+    if not x.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if not x.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _validate(Q: torch.Tensor, K_mat: torch.Tensor, V: torch.Tensor) -> None:
+    _check_input(Q, "Q")
+    _check_input(K_mat, "K_mat")
+    _check_input(V, "V")
+    if Q.dtype != torch.bfloat16:  # torch_bind.cpp:33-42 dispatches on Q's dtype only
+        raise RuntimeError("Unsupported tensor dtype. Use bfloat16.")
+    # Checks the reference leaves out (its kernel silently assumes them).
+    if K_mat.dtype != torch.bfloat16 or V.dtype != torch.bfloat16:
+        raise RuntimeError("Unsupported tensor dtype. Use bfloat16.")
+    if Q.dim() != 4:
+        raise RuntimeError(f"Q must be 4-D (batch, heads, seq_len, head_dim), got shape {tuple(Q.shape)}")
+    if K_mat.shape != Q.shape or V.shape != Q.shape:
+        raise RuntimeError(
+            f"Q, K_mat and V must have the same shape, got {tuple(Q.shape)}, "
+            f"{tuple(K_mat.shape)}, {tuple(V.shape)}"
+        )
+    if K_mat.device != Q.device or V.device != Q.device:
+        raise RuntimeError("Q, K_mat and V must be on the same device")
+    if Q.shape[3] != HEAD_DIM:
+        raise RuntimeError(f"head_dim must be {HEAD_DIM}, got {Q.shape[3]}")
+
+
+def _launch(Q, K_mat, V, O, lse, softmax_scale: float, causal: bool) -> None:
+    B, H, N, D = Q.shape
+    with torch.cuda.device(Q.device):
+        stream = torch.cuda.current_stream(Q.device).cuda_stream
+        _C.fwd(
+            Q.data_ptr(), K_mat.data_ptr(), V.data_ptr(), O.data_ptr(),
+            0 if lse is None else lse.data_ptr(),
+            B, H, N, D, float(softmax_scale), bool(causal), stream,
+        )
+
+
+def forward(Q: torch.Tensor, K_mat: torch.Tensor, V: torch.Tensor, /) -> torch.Tensor:
+    """Causal attention forward, ``softmax(Q K^T / sqrt(d)) V`` per (batch, head).
+
+    Same call as the reference's ``custom_flash_attn.forward`` (torch_bind.cpp:21-45):
+    positional Q, K_mat, V, each a contiguous bf16 CUDA(HIP) tensor of shape
+    (B, H, N, 64); returns a new O of the same shape and dtype.  Errors raise
+    RuntimeError with the reference's messages for device, contiguity and dtype.
+    """
+    _validate(Q, K_mat, V)
+    O = torch.empty_like(Q)
+    _launch(Q, K_mat, V, O, None, 1.0 / math.sqrt(Q.shape[3]), True)
+    return O
+
+
+def forward_lse(Q: torch.Tensor, K_mat: torch.Tensor, V: torch.Tensor, /,
+                softmax_scale: float | None = None, causal: bool = True):
+    """Like :func:`forward`, also returning the natural-log log-sum-exp.
+
+    Returns ``(O, LSE)`` with LSE of shape (B, H, N), float32:
+    ``LSE[b,h,i] = log(sum_{j<=i} exp(scale * q_i . k_j))`` - the ``lse_i`` of
+    src/py/triton_implementation.py:153-154.  ``softmax_scale`` defaults to
+    1/sqrt(head_dim) as in triton_implementation.py:197; ``causal=False`` drops the
+    mask (all keys attend).
+    """
+    _validate(Q, K_mat, V)
+    scale = (1.0 / math.sqrt(Q.shape[3])) if softmax_scale is None else float(softmax_scale)
+    O = torch.empty_like(Q)
+    lse = torch.empty(Q.shape[:3], dtype=torch.float32, device=Q.device)
+    _launch(Q, K_mat, V, O, lse, scale, causal)
+    return O, lse
+
+
+def device_info() -> dict:
+    """CU count, shader clock (MHz) and gfx arch of the current device (cached per device)."""
+    return _C.device_info()

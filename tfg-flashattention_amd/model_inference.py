@@ -1,0 +1,237 @@
+"""GPT-2 model whose attention can run on the MI355X kernel - the caller of the hot path.
+
+Mirrors the reference's model classes (src/py/model_inference.py:39-190) with the same
+names, constructor arguments and config keys, so code written against the reference's
+``GPTModel(cfg)`` runs unchanged.  Only the parts needed to run a forward pass are
+here; the reference's data loader, decoding loop, training helpers and pretrained-weight
+download (model_inference.py:23-37, :193-376; gpt_download.py) are not.
+
+``impl_type`` selects the attention implementation as at model_inference.py:68-90:
+  * ``"manual"``     - the reference's explicit PyTorch path (:68-75);
+  * ``"functional"`` - torch.nn.functional.scaled_dot_product_attention (:77-80);
+  * ``"hip"`` (``"cuda"`` accepted as the reference's spelling) - custom_flash_attn.forward,
+    the hand-written gfx950 kernel (:85-90).  There is no fallback: if the extension is
+    missing this raises.
+  * ``"triton"`` is not provided (the Triton variant is not rebuilt).
+
+Behaviour difference, on purpose: the reference's "cuda" branch reshapes the kernel's
+(B, H, N, d) output straight to (B, N, H*d) without transposing (model_inference.py:92),
+which scrambles heads and tokens.  Here the kernel output is transposed back to
+(B, N, H, d) first, as the "manual" and "functional" branches do (:75, :80), so all
+implementations compute the same function.
+"""
+from __future__ import annotations
+
+import math
+from typing import Callable, Dict
+
+import torch
+import torch.nn as nn
+from torch.nn import functional as F
+
+# --------------------------------------------------------------------------------------
+# Attention implementations: (queries, keys, values, mask_bool, dropout) -> (B, N, H, d).
+# queries/keys/values arrive as (B, H, N, d) views (model_inference.py:64-66).
+
+
+def _attn_manual(q, k, v, mask_bool, dropout):
+    # model_inference.py:68-75
+    attn = q @ k.transpose(-2, -1)
+    attn.masked_fill_(mask_bool, -torch.inf)
+    attn_weights = torch.softmax(attn / k.shape[-1] ** 0.5, dim=-1)
+    attn_weights = dropout(attn_weights)
+    return (attn_weights @ v).transpose(1, 2)
+
+
+def _attn_functional(q, k, v, mask_bool, dropout):
+    # model_inference.py:77-80
+    p = dropout.p if dropout.training else 0.0
+    return F.scaled_dot_product_attention(q, k, v, is_causal=True, dropout_p=p).transpose(1, 2)
+
+
+def _attn_hip(q, k, v, mask_bool, dropout):
+    # model_inference.py:85-90, plus the transpose back to (B, N, H, d).
+    import custom_flash_attn  # raises if the native extension is not built
+
+    out = custom_flash_attn.forward(q.contiguous(), k.contiguous(), v.contiguous())
+    return out.transpose(1, 2)
+
+
+ATTENTION_IMPLS: Dict[str, Callable] = {
+    "manual": _attn_manual,
+    "functional": _attn_functional,
+    "hip": _attn_hip,
+    "cuda": _attn_hip,
+}
+
+
+class MultiHeadAttention(nn.Module):
+    """Causal multi-head self-attention (model_inference.py:39-94)."""
+
+    def __init__(self, d_in, d_out, context_length, dropout, num_heads, impl_type, qkv_bias=False):
+        super().__init__()
+        assert d_out % num_heads == 0, "The output dimension must be a multiplicand of num_heads"
+        if impl_type not in ATTENTION_IMPLS:
+            raise ValueError(
+                f"impl_type {impl_type!r} not available; choose one of {sorted(ATTENTION_IMPLS)}"
+            )
+        self.head_dim = d_out // num_heads
+        self.num_heads = num_heads
+        self.d_out = d_out
+        self.impl_type = impl_type
+        self.W_query = nn.Linear(d_in, d_out, bias=qkv_bias)
+        self.W_key = nn.Linear(d_in, d_out, bias=qkv_bias)
+        self.W_value = nn.Linear(d_in, d_out, bias=qkv_bias)
+        self.out_proj = nn.Linear(d_out, d_out)
+        self.dropout = nn.Dropout(dropout)
+        self.register_buffer(
+            "mask", torch.triu(torch.ones(context_length, context_length), diagonal=1)
+        )
+
+    def forward(self, x):
+        b, num_tokens, _ = x.shape
+        queries = self.W_query(x)
+        keys = self.W_key(x)
+        values = self.W_value(x)
+        keys = keys.view(b, num_tokens, self.num_heads, self.head_dim).transpose(1, 2)
+        queries = queries.view(b, num_tokens, self.num_heads, self.head_dim).transpose(1, 2)
+        values = values.view(b, num_tokens, self.num_heads, self.head_dim).transpose(1, 2)
+        mask_bool = self.mask.bool()[:num_tokens, :num_tokens]
+        context_vec = ATTENTION_IMPLS[self.impl_type](queries, keys, values, mask_bool, self.dropout)
+        context_vec = context_vec.contiguous().view(b, num_tokens, self.d_out)
+        return self.out_proj(context_vec)
+
+
+class LayerNorm(nn.Module):
+    """LayerNorm with eps 1e-5 and biased variance (model_inference.py:96-107)."""
+
+    def __init__(self, config):
+        super().__init__()
+        self.eps = 1e-5
+        self.scale = nn.Parameter(torch.ones(config["emb_dim"]))
+        self.shift = nn.Parameter(torch.zeros(config["emb_dim"]))
+
+    def forward(self, x):
+        mean = torch.mean(x, dim=-1, keepdim=True)
+        variance = torch.var(x, dim=-1, keepdim=True, unbiased=False)
+        norm_x = (x - mean) / torch.sqrt(variance + self.eps)
+        return norm_x * self.scale + self.shift
+
+
+class GELU(nn.Module):
+    """tanh-approximation GELU (model_inference.py:109-117)."""
+
+    def forward(self, x):
+        return 0.5 * x * (1 + torch.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * torch.pow(x, 3))))
+
+
+class FeedForward(nn.Module):
+    """Linear(d, 4d) -> GELU -> Linear(4d, d) (model_inference.py:119-128)."""
+
+    def __init__(self, config):
+        super().__init__()
+        self.layers = nn.Sequential(
+            nn.Linear(config["emb_dim"], 4 * config["emb_dim"]),
+            GELU(),
+            nn.Linear(4 * config["emb_dim"], config["emb_dim"]),
+        )
+
+    def forward(self, x):
+        return self.layers(x)
+
+
+class TransformerBlock(nn.Module):
+    """Pre-LN block; attention runs under bf16 autocast on the GPU (model_inference.py:131-164)."""
+
+    def __init__(self, cfg):
+        super().__init__()
+        self.att = MultiHeadAttention(
+            d_in=cfg["emb_dim"], d_out=cfg["emb_dim"], context_length=cfg["context_length"],
+            num_heads=cfg["n_heads"], dropout=cfg["drop_rate"], impl_type=cfg["impl_type"],
+            qkv_bias=cfg["qkv_bias"],
+        )
+        self.ff = FeedForward(cfg)
+        self.norm1 = LayerNorm(cfg)
+        self.norm2 = LayerNorm(cfg)
+        self.drop_shortcut = nn.Dropout(cfg["drop_rate"])
+
+    def forward(self, x):
+        shortcut = x
+        x = self.norm1(x)
+        # model_inference.py:153 - autocast only has an effect for CUDA(HIP) tensors, so it
+        # is switched on only for them (same result, no warning on CPU-only hosts).
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16, enabled=x.is_cuda):
+            x = self.att(x)
+        x = self.drop_shortcut(x)
+        x = x + shortcut
+        shortcut = x
+        x = self.norm2(x)
+        x = self.ff(x)
+        x = self.drop_shortcut(x)
+        return x + shortcut
+
+
+class GPTModel(nn.Module):
+    """Token + position embeddings, blocks, final LN, untied LM head (model_inference.py:166-190)."""
+
+    def __init__(self, cfg):
+        super().__init__()
+        self.tok_emb = nn.Embedding(cfg["vocab_size"], cfg["emb_dim"])
+        self.pos_emb = nn.Embedding(cfg["context_length"], cfg["emb_dim"])
+        self.drop_emb = nn.Dropout(cfg["drop_rate"])
+        self.trf_blocks = nn.Sequential(*[TransformerBlock(cfg) for _ in range(cfg["n_layers"])])
+        self.final_norm = LayerNorm(cfg)
+        self.out_head = nn.Linear(cfg["emb_dim"], cfg["vocab_size"], bias=False)
+
+    def forward(self, in_idx):
+        _, seq_len = in_idx.shape
+        tok_embeds = self.tok_emb(in_idx)
+        pos_embeds = self.pos_emb(torch.arange(seq_len, device=in_idx.device))
+        x = self.drop_emb(tok_embeds + pos_embeds)
+        x = self.trf_blocks(x)
+        x = self.final_norm(x)
+        return self.out_head(x)
+
+
+# Base config (model_inference.py:378-386) and the sizes of model_inference.py:393-397; the
+# benchmark loop sets context_length 1024 and qkv_bias True (:415).
+GPT_CONFIG_124M = {
+    "vocab_size": 50257,
+    "context_length": 256,
+    "emb_dim": 768,
+    "n_heads": 12,
+    "n_layers": 12,
+    "drop_rate": 0.1,
+    "qkv_bias": False,
+}
+
+MODEL_CONFIGS = {
+    "gpt2-small (124M)": {"emb_dim": 768, "n_layers": 12, "n_heads": 12},
+    "gpt2-medium (355M)": {"emb_dim": 1024, "n_layers": 24, "n_heads": 16},
+    "gpt2-large (774M)": {"emb_dim": 1280, "n_layers": 36, "n_heads": 20},
+    "gpt2-xl (1558M)": {"emb_dim": 1600, "n_layers": 48, "n_heads": 25},
+}
+
+
+def gpt2_config(name: str, impl_type: str, drop_rate: float = 0.0) -> dict:
+    """Config as the reference's benchmark builds it (model_inference.py:413-415)."""
+    cfg = dict(GPT_CONFIG_124M)
+    cfg.update(MODEL_CONFIGS[name])
+    cfg.update({"context_length": 1024, "qkv_bias": True, "impl_type": impl_type, "drop_rate": drop_rate})
+    return cfg
+
+
+def init_gpt2_weights(model: nn.Module, seed: int) -> None:
+    """Seeded random init in place of the pretrained download: every Linear/Embedding
+    weight ~ N(0, 0.02^2), biases 0, LayerNorm scale 1 and shift 0."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    with torch.no_grad():
+        for mod in model.modules():
+            if isinstance(mod, (nn.Linear, nn.Embedding)):
+                w = torch.empty(mod.weight.shape, dtype=torch.float32).normal_(0.0, 0.02, generator=g)
+                mod.weight.copy_(w)
+                if getattr(mod, "bias", None) is not None:
+                    mod.bias.zero_()
+            elif isinstance(mod, LayerNorm):
+                mod.scale.fill_(1.0)
+                mod.shift.zero_()
