@@ -45,9 +45,9 @@ def bytes_per_fwd(b=B, h=H, n=N, d=D):
 
 def cpu_baseline(gpu_o_sample, q_sample, k_sample, v_sample, heads_in_sample):
     """Times the reference's PyTorch CPU "manual" attention (fp32) on a sample of the
-    workload: the first `heads_in_sample` (b, h) heads of input set 0, full N.  Reports
-    TFLOP/s with the same algorithmic FLOP count (the manual path itself computes the full
-    N x N matrix, twice that)."""
+    workload: `heads_in_sample` (b, h) heads of input set 0 (all 200 by default, i.e. the
+    whole config), full N.  Reports TFLOP/s with the same algorithmic FLOP count (the manual
+    path itself computes the full N x N matrix, twice that)."""
     import torch
 
     from oracle import manual_attention_torch
@@ -70,9 +70,9 @@ def cpu_baseline(gpu_o_sample, q_sample, k_sample, v_sample, heads_in_sample):
         "unit": "TFLOP/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"{heads_in_sample} of {B * H} heads (B=1 x H={heads_in_sample}, N={N}, d={D}) of "
-                   f"the bench inputs, torch {torch.__version__} fp32 manual path, median of 3 runs "
-                   f"= {sec:.3f} s; same algorithmic FLOPs per head as the GPU figure"),
+        "sample": (f"{heads_in_sample} of {B * H} (batch, head) pairs, N={N}, d={D}, of bench input "
+                   f"set 0; torch {torch.__version__} fp32 manual path on {cores} threads, median of "
+                   f"3 runs = {sec:.3f} s; TFLOP/s on the same algorithmic FLOP count as the GPU"),
         "seconds_per_sample": sec,
         "max_abs_diff_vs_gpu": max_err,
     }
@@ -84,8 +84,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=25,
+    ap.add_argument("--cpu-heads", type=int, default=200,
                     help="heads of the workload timed by the CPU baseline")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run 5 plain device-to-device copies of MIB "
+                         "MiB (the reference kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -103,6 +106,15 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "copies": 5}))
+        return
     info = custom_flash_attn.device_info()
 
     gen = torch.Generator(device=dev).manual_seed(1003)
@@ -168,10 +180,10 @@ def main():
         "device": info,
     }
     if not args.no_cpu_baseline:
-        nh = max(1, min(args.cpu_heads, H))
-        q, k, v, o, _ = sets[0]
+        nh = max(1, min(args.cpu_heads, B * H))
+        q, k, v, o = (t.reshape(1, B * H, N, D)[:, :nh] for t in sets[0][:4])
         torch.cuda.synchronize()
-        result["cpu_baseline"] = cpu_baseline(o[:1, :nh], q[:1, :nh], k[:1, :nh], v[:1, :nh], nh)
+        result["cpu_baseline"] = cpu_baseline(o, q, k, v, nh)
     print(json.dumps(result), flush=True)
 
 

@@ -59,7 +59,8 @@ extern "C" {
  * default stream (v1.cu:33-34).  Here the scale is explicit (pass 0.125 for
  * the reference's behaviour), `lse` may be NULL, and `hip_stream` (a
  * hipStream_t, NULL = default stream) is the stream the caller is using.
- * B, H or N equal to 0 is an empty problem: nothing is launched, 0 returned.
+ * B, H or N equal to 0 is an empty problem: nothing is launched and 0 is returned,
+ * whatever the pointers are (an empty torch tensor's data pointer is NULL).
  */
 int tfgfa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
                    int B, int H, int N, int D, float softmax_scale, int causal,

@@ -84,6 +84,8 @@ P = 0x10000
     ((P, P, P, P, 0, 1, 1, 1 << 30, 64, 0.125, 1), "TFGFA_ERR_TOO_LARGE"),
     ((P, P, P, P, 0, 0, 4, 16, 64, 0.125, 1), "TFGFA_OK"),   # empty problem: nothing launched
     ((P, P, P, P, 0, 2, 4, 0, 64, 0.125, 0), "TFGFA_OK"),
+    ((0, 0, 0, 0, 0, 2, 4, 0, 64, 0.125, 1), "TFGFA_OK"),     # empty tensors have NULL data
+    ((0, 0, 0, 0, 0, 2, 4, 0, 128, 0.125, 1), "TFGFA_ERR_HEAD_DIM"),  # sizes checked first
 ])
 def test_c_abi_argument_validation(lib, args, code):
     assert lib.tfgfa_fwd_bf16(*args, None) == _header_define(code)

@@ -317,20 +317,24 @@ constexpr int kMaxDevices = 64;
 static std::once_flag g_dev_once[kMaxDevices];
 static DeviceInfo g_dev_info[kMaxDevices];
 
+// Argument checks, in this order: sizes and flags first, then - only for a non-empty
+// problem - pointers.  An empty tensor may legitimately have a null data pointer
+// (torch gives numel()==0 tensors address 0), so B, H or N == 0 succeeds with no launch.
 static int validate(const void* q, const void* k, const void* v, const void* o, const float* lse,
                     int B, int H, int N, int D, float scale, int causal) {
-  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr) return TFGFA_ERR_NULL_POINTER;
   if (B < 0 || H < 0 || N < 0) return TFGFA_ERR_BAD_SHAPE;
   if (D != kD) return TFGFA_ERR_HEAD_DIM;
   if (!(scale > 0.f) || !isfinite(scale)) return TFGFA_ERR_SCALE;
   if (causal != 0 && causal != 1) return TFGFA_ERR_CAUSAL_FLAG;
+  if (B == 0 || H == 0 || N == 0) return TFGFA_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr) return TFGFA_ERR_NULL_POINTER;
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15u) return TFGFA_ERR_ALIGNMENT;
   if (((uintptr_t)lse) & 3u) return TFGFA_ERR_ALIGNMENT;
   const long long bh = (long long)B * H;
   const long long nqb = ((long long)N + kBlockRows - 1) / kBlockRows;
   if (bh > INT32_MAX || bh * nqb > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
   // Per-head byte offsets (row * 128 B) are 32-bit buffer offsets.
-  if ((long long)(N + kBlockRows) * kKRowBytes > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
+  if (((long long)N + kBlockRows) * kKRowBytes > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
   return TFGFA_OK;
 }
 
