@@ -87,8 +87,8 @@ def main():
     ap.add_argument("--cpu-heads", type=int, default=200,
                     help="heads of the workload timed by the CPU baseline")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
-                    help="instead of the benchmark, run 5 plain device-to-device copies of MIB "
-                         "MiB (the reference kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
+                    help="instead of the benchmark, run 5 fp32->bf16 copy kernels over MIB MiB "
+                         "(known bytes, for scaling the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -107,13 +107,16 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.calibrate_copy:
+        # An fp32 -> bf16 conversion copy runs as a kernel (a same-dtype copy_ would be a DMA
+        # transfer, invisible to the TCC counters): it reads 4 B and writes 2 B per element.
         n = args.calibrate_copy * (1 << 20) // 4
         src = torch.ones(n, device=dev, dtype=torch.float32)
-        dst = torch.empty_like(src)
+        dst = torch.empty(n, device=dev, dtype=torch.bfloat16)
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "copies": 5}))
+        print(json.dumps({"kernel": "bfloat16_copy_kernel", "bytes_read": n * 4,
+                          "bytes_written": n * 2, "copies": 5}))
         return
     info = custom_flash_attn.device_info()
 
