@@ -10,19 +10,28 @@
 //
 // Work decomposition
 //   One workgroup = 4 waves = one 128-row query block of one (batch, head).  Each wave owns
-//   32 query rows and walks the key/value sequence in 64-key tiles.  Tiles wholly above the
-//   causal diagonal are never loaded (per workgroup) or computed (per wave); only tiles that
-//   cross the diagonal or the sequence end apply an element mask.  Workgroups are issued
-//   heaviest query block first.
+//   32 query rows.  Keys are staged in 64-key tiles but processed in 32-key halves, which line
+//   up with the wave's 32 rows: a half is either wholly visible, wholly above the causal
+//   diagonal (never computed) or the single diagonal block (element mask).  Tiles wholly above
+//   the diagonal of the whole block are never loaded.  Workgroups are issued heaviest query
+//   block first.
+//
+// Per-wave software pipeline (32-key halves u = 0, 1, ...)
+//   half-step u:  O += V_{u-1} P_{u-1}   together with   row max of S_u
+//                 (rescale O, l if the max moved: rare, lazy)
+//                 S_{u+1} = K_{u+1} Q^T  together with   P_u = exp2(S_u - m), l += rowsum
+//   Each MFMA group shares a basic block with VALU work that does not depend on it, so the
+//   MFMA pipe and the VALU stay busy at the same time; the S double buffer is 2 x 16
+//   registers, which keeps three waves per SIMD.
 //
 // Memory pipeline
 //   K and V tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds: each lane's
-//   16 B land at LDS base + 16*lane), through a ring of 3 stages, so two tiles are in flight
-//   while one is computed.  No registers or VALU work are spent on staging.  Loads past the
-//   sequence end return zero (buffer range check), which is the zero-fill of partial tiles.
-//   One barrier per tile: wait for this wave's loads of the tile, barrier (all waves' loads
-//   landed, all waves done with the stage about to be refilled), issue the loads two tiles
-//   ahead, compute.
+//   16 B land at LDS base + 16*lane), no registers or VALU spent on staging.  Two rings of 3
+//   slots (K, V).  Tile step j: issue K_{j+2} and V_{j+1}; half-step 2j (uses K_j, V_{j-1});
+//   wait for this wave's loads of K_{j+1} and V_j and barrier; half-step 2j+1 (uses K_{j+1},
+//   V_j).  The barrier also proves every wave has finished with the slots refilled at step j+1.
+//   Loads past the sequence end return zero (buffer range check): the zero-fill of partial
+//   tiles.
 //
 // MFMA chaining without an LDS round trip (v_mfma_f32_32x32x16_bf16, fp32 accumulate)
 //   S^T = K . Q^T  : A = K tile rows (32 keys x 16 d, ds_read_b128), B = Q^T (16 d x 32
@@ -42,9 +51,10 @@
 //   one d, the V^T operand layout.
 //
 // LDS layouts (per stage: K tile 8 KiB then V tile 8 KiB, 128 B per key row)
-//   16-B chunk c of row r is stored at chunk c ^ swz(r).  K: swz = (r ^ (r >> 3)) & 7 makes any
-//   8 (or 16) consecutive rows of one logical chunk hit distinct banks for the ds_read_b128
-//   A-operand reads.  V: swz = 2*(r & 3) makes the 4-row x 32-B footprint of a transposing read
+//   16-B chunk c of row r is stored at chunk c ^ swz(r).  K: swz = (r ^ ((r >> 3) & 3)) & 7
+//   makes any 8 (or 16) consecutive rows of one logical chunk hit distinct banks for the
+//   ds_read_b128 A-operand reads, and is the same for rows r and r + 32, so the two key halves
+//   of a tile differ by an immediate offset.  V: swz = 2*(r & 3) makes the 4-row x 32-B footprint of a transposing read
 //   group (and of two groups side by side) hit distinct banks.
 //
 // Softmax runs in the exp2 domain: scores are scaled by scale*log2(e) inside one FMA, the
@@ -77,7 +87,6 @@ constexpr int kKRowBytes = kD * 2;          // 128 B per K or V row
 constexpr int kHalfTileBytes = kTileKeys * kKRowBytes;  // 8 KiB (K or V)
 constexpr int kTileBytes = 2 * kHalfTileBytes;          // 16 KiB per stage
 constexpr int kStages = 3;
-constexpr int kSmemBytes = kStages * kTileBytes;        // 48 KiB
 constexpr int kLoadsPerWave = 2 * (kHalfTileBytes / 1024) / kWaves;  // 1 KiB per load instr: 4
 
 // The running max used as the exp2 offset is only moved when a row's tile max exceeds it by
@@ -106,37 +115,67 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ int swz_k(int row) { return (row ^ (row >> 3)) & 7; }
+__device__ __forceinline__ int swz_k(int row) { return (row ^ ((row >> 3) & 3)) & 7; }
 __device__ __forceinline__ int swz_v(int row) { return (row & 3) << 1; }
 
-// Buffer resource over one head's (N, 64) bf16 rows: loads at byte offsets >= N*128 return
-// zero.  The whole offset is kept in the VGPR operand so the range check covers all of it.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const __bf16* base, int N) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(base), (short)0, N * kKRowBytes,
-                                           0x00020000);
+// Buffer descriptor over one head's (N, 64) bf16 rows, as four SGPRs for the loads issued from
+// inline assembly: base address, stride 0, num_records = N * 128 bytes, format word 0x20000
+// (the layout __builtin_amdgcn_make_buffer_rsrc builds for the Q loads).  A raw buffer load whose
+// byte offset is at or past num_records returns zero: that is the zero-fill of tiles and query
+// blocks past the sequence end.  The whole offset is kept in the VGPR operand so the range
+// check covers all of it.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x4 head_desc(const __bf16* base, int N) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  i32x4 d;
+  d[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  d[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  d[2] = N * kKRowBytes;
+  d[3] = 0x00020000;
+  return d;
 }
 
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, int byte_off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+// One 1-KiB HBM -> LDS transfer: lane i's 16 B (global byte offset `voff` in the buffer) land at
+// LDS byte address lds_base + 16*i.  Issued from inline assembly so that the compiler does not
+// track it: it would otherwise wait for every outstanding transfer before LDS reads it cannot
+// prove disjoint (it loses that proof at control-flow joins).  The only waits on these
+// transfers are the explicit vmcnt waits of the pipeline.
+__device__ __forceinline__ void lds_transfer(i32x4 desc, uint32_t lds_base, int voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds_base), "v"(voff), "s"(desc)
+      : "memory", "m0");
 }
 
-// This wave's share of one tile: K and V rows [8*(2w), 8*(2w+2)) as 1-KiB LDS blocks.  Lane i
-// of a block fills physical chunk i%8 of row i/8, so it fetches the logical chunk that the
-// swizzle maps there.
-__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
-                                           unsigned char* stage, int k0, int wave, int lane) {
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
+  return (uint32_t)(uintptr_t)(const lds_void*)p;
+}
+
+// This wave's share of one K (or V) tile: rows [8*(2w), 8*(2w+2)) as two 1-KiB LDS blocks.
+// Lane i of a block fills physical chunk i%8 of row i/8, so it fetches the logical chunk that
+// the swizzle maps there.
+template <bool kIsV>
+__device__ __forceinline__ void issue_half(i32x4 desc, unsigned char* dst, int k0, int wave,
+                                           int lane) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int blk = 2 * wave + i;
     const int row = blk * 8 + (lane >> 3);
     const int pc = lane & 7;
-    const int goff = (k0 + row) * kKRowBytes;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_void*)(stage + blk * 1024), 16,
-                                             goff + ((pc ^ swz_k(row)) << 4), 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_void*)(stage + kHalfTileBytes + blk * 1024),
-                                             16, goff + ((pc ^ swz_v(row)) << 4), 0, 0, 0);
+    const int sw = kIsV ? swz_v(row) : swz_k(row);
+    lds_transfer(desc, lds_addr(dst + blk * 1024), (k0 + row) * kKRowBytes + ((pc ^ sw) << 4));
   }
 }
+
+// Workgroup barrier that is also a compiler memory barrier: no LDS access moves across it (the
+// s_barrier builtin alone is not a memory operation for the optimizer), and unlike
+// __syncthreads() it adds no wait for outstanding vector memory loads, which would drain the
+// load pipeline.  The only LDS writes are the buffer_load ... lds transfers, completed by the
+// explicit vmcnt waits before each barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -144,63 +183,89 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Per-wave state carried across tiles.
+// LDS: a ring of 3 K tiles and a ring of 3 V tiles, each slot its own __shared__ array.  The
+// compiler tracks the buffer_load ... lds transfers and waits for every one of them before an
+// LDS read it cannot prove disjoint; with one array per slot, a transfer into one slot does
+// not hold up reads of another, so the explicit per-step waits are the only ones.
+struct Lds {
+  unsigned char* k[kStages];
+  unsigned char* v[kStages];
+};
+
+// Per-wave state carried across half-steps.
 struct WaveState {
   bf16x8 qop[4];   // Q^T operand: Q[qrow][16c + 8h .. +7]
   f32x16 o0, o1;   // O^T accumulators: d = 0..31 and d = 32..63
+  f32x16 s;        // S^T of the half being softmaxed: register t = key 8(t/4) + 4h + t%4
+  bf16x8 pb[2];    // P^T (bf16) of the previous half, waiting for its P.V
   float m_run;     // exp2 offset (running max of scale*log2e*s, moved lazily)
   float l_run;     // running sum of exp2(scale*log2e*s - m_run)
-  int koff[2][4];  // K A-operand LDS offsets (within a stage)
-  int voff[2][2];  // V^T transposing-read LDS offsets (within a stage, c4 = 0)
+  int koff[4];     // K A-operand LDS offsets (within a K slot, key half 0)
+  int voff[2][2];  // V^T transposing-read LDS offsets (within a V slot, keys 0..15)
 };
 
-// One 64-key tile for one wave: S^T = K Q^T, mask (kMask), online softmax, O^T += V^T P^T.
-// kStage is the LDS ring slot, so every LDS address is a per-lane base plus an immediate.
-template <int kStage, bool kMask>
-__device__ __forceinline__ void tile_step(WaveState& w, const unsigned char* smem, int lim,
-                                          float scale_log2) {
-  const unsigned char* stage = smem + kStage * kTileBytes;
-
-  // S^T for keys k0 + [0,32) (s0) and k0 + [32,64) (s1).
-  f32x16 s0, s1;
+// S^T = K Q^T for key half kHalf of the tile in K slot kSlot (4 MFMAs).
+template <int kSlot, int kHalf>
+__device__ __forceinline__ f32x16 qk_half(const WaveState& w, const Lds& lds) {
+  const unsigned char* kt = lds.k[kSlot] + kHalf * 32 * kKRowBytes;
+  f32x16 acc;
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    s0[t] = 0.f;
-    s1[t] = 0.f;
-  }
+  for (int t = 0; t < 16; ++t) acc[t] = 0.f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(stage + w.koff[0][c]);
-    const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(stage + w.koff[1][c]);
-    s0 = mfma32(a0, w.qop[c], s0);
-    s1 = mfma32(a1, w.qop[c], s1);
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + w.koff[c]);
+    acc = mfma32(a, w.qop[c], acc);
   }
+  return acc;
+}
 
-  // Register t of s0 is key k0 + 8(t/4) + 4h + t%4 (s1: +32); lim is the last visible key of
-  // the lane's row relative to k0 + 4h.
-  if (kMask) {
+// O^T += V^T P^T for key half kHalf of the tile in V slot kSlot, with P^T = w.pb (4 MFMAs).
+// Element e of chunk cc in lane half h is key 16*cc + 8*(e/4) + 4*h + e%4 of the key half:
+// two transposing reads of 4 keys each.
+template <int kSlot, int kHalf>
+__device__ __forceinline__ void pv_half(WaveState& w, const Lds& lds) {
+  const unsigned char* vt = lds.v[kSlot] + kHalf * 32 * kKRowBytes;
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int kk = 8 * (t >> 2) + (t & 3);
-      s0[t] = kk > lim ? -INFINITY : s0[t];
-      s1[t] = kk + 32 > lim ? -INFINITY : s1[t];
+  for (int cc = 0; cc < 2; ++cc) {
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(vt + w.voff[dt][0] + cc * 16 * kKRowBytes));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(vt + w.voff[dt][1] + cc * 16 * kKRowBytes));
+      const bf16x8 va =
+          __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      if (dt == 0)
+        w.o0 = mfma32(va, w.pb[cc], w.o0);
+      else
+        w.o1 = mfma32(va, w.pb[cc], w.o1);
     }
   }
+}
 
-  // Row max over this lane's 32 scores, then across the lane pair.
-  float mx = fmaxf(s0[0], fmaxf(s0[1], s0[2]));
+// Masks w.s past the last visible key; lim is the lane's last visible key relative to the
+// half's first key + 4h.
+__device__ __forceinline__ void mask_half(WaveState& w, int lim) {
 #pragma unroll
-  for (int t = 3; t < 15; t += 2) mx = fmaxf(mx, fmaxf(s0[t], s0[t + 1]));
-  mx = fmaxf(mx, fmaxf(s0[15], s1[0]));
-#pragma unroll
-  for (int t = 1; t < 15; t += 2) mx = fmaxf(mx, fmaxf(s1[t], s1[t + 1]));
-  mx = fmaxf(mx, s1[15]);
-  mx = pair_max(mx);
+  for (int t = 0; t < 16; ++t) {
+    const int kk = 8 * (t >> 2) + (t & 3);
+    w.s[t] = kk > lim ? -INFINITY : w.s[t];
+  }
+}
 
-  // Lazy rescale: every active tile has an unmasked key in every row (the tile starts at or
-  // below the wave's first row), so the tile max is finite and the first tile always moves
-  // m_run off -inf.
-  const float m_tile = mx * scale_log2;
+// Row max of w.s over the lane pair, scaled to the exp2 domain.
+__device__ __forceinline__ float row_max(const WaveState& w, float scale_log2) {
+  float mx = fmaxf(w.s[0], fmaxf(w.s[1], w.s[2]));
+#pragma unroll
+  for (int t = 3; t < 15; t += 2) mx = fmaxf(mx, fmaxf(w.s[t], w.s[t + 1]));
+  mx = fmaxf(mx, w.s[15]);
+  return pair_max(mx) * scale_log2;
+}
+
+// Lazy rescale of O and l when the row max moved by more than the threshold.  Every computed
+// half has an unmasked key in every row (it starts at or below the wave's first row), so the
+// max is finite and the first half always moves m_run off -inf.
+__device__ __forceinline__ void rescale(WaveState& w, float m_tile) {
   const bool grow = m_tile > w.m_run + kRescaleThreshold;
   if (__builtin_amdgcn_ballot_w64(grow) != 0) {
     const float m_new = grow ? m_tile : w.m_run;
@@ -213,85 +278,95 @@ __device__ __forceinline__ void tile_step(WaveState& w, const unsigned char* sme
       w.o1[t] *= alpha;
     }
   }
+}
 
-  // P = exp2(scale*log2e*s - m_run) in fp32; the row sum l is taken in fp32 (four partial
-  // sums to shorten the dependency chain), then P is rounded to bf16 for the MFMA.
-  // Chunk c4 covers keys 16*c4 .. 16*c4+15 of the tile; this lane's 8 values are
-  // accumulator registers 8*(c4&1) .. +7 of s0 (c4 < 2) or s1.
+// P = exp2(scale*log2e*s - m_run) in fp32, row sum into l (two partial sums), P rounded to
+// bf16 into w.pb: chunk cc (keys 16cc .. 16cc+15 of the half) is registers 8cc .. 8cc+7.
+__device__ __forceinline__ void exp_half(WaveState& w, float scale_log2) {
   const float neg_m = -w.m_run;
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    s0[t] = __builtin_amdgcn_exp2f(fmaf(s0[t], scale_log2, neg_m));
-    s1[t] = __builtin_amdgcn_exp2f(fmaf(s1[t], scale_log2, neg_m));
-  }
-  float ps0 = s0[0], ps1 = s0[1], ps2 = s1[0], ps3 = s1[1];
+  for (int t = 0; t < 16; ++t) w.s[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, neg_m));
+  float ps0 = w.s[0], ps1 = w.s[1];
 #pragma unroll
   for (int t = 2; t < 16; t += 2) {
-    ps0 += s0[t];
-    ps1 += s0[t + 1];
-    ps2 += s1[t];
-    ps3 += s1[t + 1];
+    ps0 += w.s[t];
+    ps1 += w.s[t + 1];
   }
-  w.l_run += pair_sum((ps0 + ps1) + (ps2 + ps3));
-  bf16x8 pb[4];
+  w.l_run += pair_sum(ps0 + ps1);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    pb[0][e] = (__bf16)s0[e];
-    pb[1][e] = (__bf16)s0[8 + e];
-    pb[2][e] = (__bf16)s1[e];
-    pb[3][e] = (__bf16)s1[8 + e];
-  }
-
-  // O^T += V^T P^T.  Element e of chunk c4 in lane half h is key 16*c4 + 8*(e/4) + 4*h + e%4:
-  // two transposing reads of 4 keys each.
-#pragma unroll
-  for (int c4 = 0; c4 < 4; ++c4) {
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(stage + w.voff[dt][0] + c4 * 16 * kKRowBytes));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(stage + w.voff[dt][1] + c4 * 16 * kKRowBytes));
-      const bf16x8 va =
-          __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      if (dt == 0)
-        w.o0 = mfma32(va, pb[c4], w.o0);
-      else
-        w.o1 = mfma32(va, pb[c4], w.o1);
-    }
+    w.pb[0][e] = (__bf16)w.s[e];
+    w.pb[1][e] = (__bf16)w.s[8 + e];
   }
 }
 
-// Pipeline step for tile j held in ring slot kStage: wait for the tile, barrier, refill the
-// slot freed by tile j-1 with tile j+2, then compute (unless the wave has no visible key).
-template <int kStage>
-__device__ __forceinline__ void pipeline_step(WaveState& w, unsigned char* smem, int j, int nT,
-                                              __amdgpu_buffer_rsrc_t k_rsrc,
-                                              __amdgpu_buffer_rsrc_t v_rsrc, int wave, int lane,
-                                              int q0, int N, int causal, int last_key, int h,
-                                              float scale_log2) {
-  if (j + 1 < nT)
-    wait_vmcnt<kLoadsPerWave>();  // tile j landed; tile j+1 may still be in flight
+// Loop-invariant inputs of the pipeline.
+struct StepArgs {
+  i32x4 k_rsrc, v_rsrc;
+  int nT;        // 64-key tiles loaded by the workgroup
+  int nAct;      // 32-key halves this wave computes (a prefix)
+  int nFull;     // halves this wave computes without an element mask (a prefix of the above)
+  int wave, lane, h, last_key;
+  float scale_log2;
+};
+
+// Half-step u: P.V of half u-1 (V slot kVs, half kVh), softmax of half u, S of half u+1 (K
+// slot kKs, half kKh).  kSteady: 1 <= u < nAct - 1 is not required, only u < nAct (a full
+// half-step) - no early exits, so each MFMA group shares a basic block with independent VALU
+// work (P.V with the row max, S_{u+1} with the exponentials):
+//  - u = 0: P is zero and the V slot read was zero-filled, so the P.V adds nothing;
+//  - S_{u+1} is computed even past the wave's last half (finite, discarded).
+// Otherwise (tail): u = nAct is the P.V of the last half only; u > nAct does nothing.
+template <int kVs, int kVh, int kKs, int kKh, bool kSteady>
+__device__ __forceinline__ void half_step(WaveState& w, const Lds& lds, int u,
+                                          const StepArgs& a) {
+  if (!kSteady && u > a.nAct) return;
+  if (u >= a.nFull && u < a.nAct) mask_half(w, a.last_key - u * 32 - 4 * a.h);
+  pv_half<kVs, kVh>(w, lds);
+  const float m_tile = row_max(w, a.scale_log2);
+  if (!kSteady && u == a.nAct) return;
+  rescale(w, m_tile);
+  const f32x16 n = qk_half<kKs, kKh>(w, lds);
+  exp_half(w, a.scale_log2);
+  w.s = n;
+}
+
+// Tile step j (slot kSlot = j % 3): issue K_{j+2}, V_{j+1}; half-step 2j; wait for K_{j+1} and
+// V_j; barrier; half-step 2j+1.
+template <int kSlot, bool kSteady>
+__device__ __forceinline__ void tile_step(WaveState& w, const Lds& lds, int j,
+                                          const StepArgs& a) {
+  constexpr int kNext = (kSlot + 1) % kStages;
+  constexpr int kNext2 = (kSlot + 2) % kStages;
+  constexpr int kPrev = (kSlot + kStages - 1) % kStages;
+  const bool k2 = j + 2 < a.nT, v1 = j + 1 < a.nT;
+  if (k2) issue_half<false>(a.k_rsrc, lds.k[kNext2], (j + 2) * kTileKeys, a.wave, a.lane);
+  if (v1) issue_half<true>(a.v_rsrc, lds.v[kNext], (j + 1) * kTileKeys, a.wave, a.lane);
+  // Half 2j: P.V of half 2j-1 (V_{j-1}, keys 32..63), S of half 2j+1 (K_j, keys 32..63).
+  half_step<kPrev, 1, kSlot, 1, kSteady>(w, lds, 2 * j, a);
+  // K_{j+1} and V_j were issued by step j-1; only this step's loads may still be in flight.
+  if (k2 && v1)
+    wait_vmcnt<kLoadsPerWave>();
+  else if (k2 || v1)
+    wait_vmcnt<kLoadsPerWave / 2>();
   else
     wait_vmcnt<0>();
-  __builtin_amdgcn_s_barrier();
-  if (j + 2 < nT)
-    issue_tile(k_rsrc, v_rsrc, smem + ((kStage + 2) % kStages) * kTileBytes, (j + 2) * kTileKeys,
-               wave, lane);
-
-  const int k0 = j * kTileKeys;
-  if (q0 >= N || (causal && k0 > q0 + kWaveRows - 1)) return;  // wave-uniform
-  if ((causal && k0 + kTileKeys - 1 > q0) || (k0 + kTileKeys > N))
-    tile_step<kStage, true>(w, smem, last_key - k0 - 4 * h, scale_log2);
-  else
-    tile_step<kStage, false>(w, smem, 0, scale_log2);
+  lds_barrier();
+  // Half 2j+1: P.V of half 2j (V_j, keys 0..31), S of half 2j+2 (K_{j+1}, keys 0..31).
+  half_step<kSlot, 0, kNext, 0, kSteady>(w, lds, 2 * j + 1, a);
 }
 
 __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
     const __bf16* __restrict__ Q, const __bf16* __restrict__ K, const __bf16* __restrict__ V,
     __bf16* __restrict__ O, float* __restrict__ LSE, int BH, int N, int nQB, float scale_log2,
     int causal) {
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[kSmemBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char k0s[kHalfTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char k1s[kHalfTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char k2s[kHalfTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char v0s[kHalfTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char v1s[kHalfTileBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char v2s[kHalfTileBytes];
+  const Lds lds = {{k0s, k1s, k2s}, {v0s, v1s, v2s}};
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -300,41 +375,64 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
   const int h = lane >> 5;
 
   // Heaviest (last) query blocks first: with causal masking block qb needs qb+1 key blocks.
+  // Workgroups are dealt to the 8 XCDs (one L2 each) round-robin, so when B*H is a multiple of
+  // 8 every query block of a head runs on the same XCD.
   const int bid = blockIdx.x;
   const int qb = nQB - 1 - bid / BH;
   const int bh = bid % BH;
 
   const size_t head_off = (size_t)bh * N * kD;
-  const __amdgpu_buffer_rsrc_t q_rsrc = head_rsrc(Q + head_off, N);
-  const __amdgpu_buffer_rsrc_t k_rsrc = head_rsrc(K + head_off, N);
-  const __amdgpu_buffer_rsrc_t v_rsrc = head_rsrc(V + head_off, N);
 
+  StepArgs a;
+  a.k_rsrc = head_desc(K + head_off, N);
+  a.v_rsrc = head_desc(V + head_off, N);
   const int q0 = qb * kBlockRows + wave * kWaveRows;  // first query row of this wave
   const int qrow = q0 + r32;                          // this lane's query row
-
   const int kv_end = causal ? min(N, (qb + 1) * kBlockRows) : N;
-  const int nT = (kv_end + kTileKeys - 1) / kTileKeys;
+  a.nT = (kv_end + kTileKeys - 1) / kTileKeys;
+  // 32-key halves computed by this wave: those starting at or below its first row (causal,
+  // q0 is a multiple of 32) and below N; unmasked: strictly below its first row (causal) and
+  // wholly below N.
+  const int nHalves = (min(N, kv_end) + 31) / 32;
+  if (q0 >= N) {
+    a.nAct = 0;
+    a.nFull = 0;
+  } else if (causal) {
+    a.nAct = min(nHalves, q0 / 32 + 1);
+    a.nFull = min(q0 / 32, N / 32);
+  } else {
+    a.nAct = nHalves;
+    a.nFull = N / 32;
+  }
+  a.nFull = min(a.nFull, a.nAct);
+  a.wave = wave;
+  a.lane = lane;
+  a.h = h;
+  a.last_key = causal ? min(qrow, N - 1) : N - 1;
+  a.scale_log2 = scale_log2;
 
-  // Start the first two tiles before anything else.
-  issue_tile(k_rsrc, v_rsrc, smem, 0, wave, lane);
-  if (nT > 1) issue_tile(k_rsrc, v_rsrc, smem + kTileBytes, kTileKeys, wave, lane);
-
+  // Q first (ordinary buffer loads, tracked by the compiler), then the prologue tiles K_0, K_1
+  // and V_0 (step j issues K_{j+2} and V_{j+1}).
   WaveState w;
+  {
+    const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<__bf16*>(Q + head_off), (short)0, N * kKRowBytes, 0x00020000);
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
-    w.qop[c] = __builtin_bit_cast(bf16x8, buf_load16(q_rsrc, qrow * kKRowBytes + 32 * c + 16 * h));
+    for (int c = 0; c < 4; ++c)
+      w.qop[c] = __builtin_bit_cast(
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(qr, qrow * kKRowBytes + 32 * c + 16 * h, 0, 0));
+  }
+  issue_half<false>(a.k_rsrc, lds.k[0], 0, wave, lane);
+  if (a.nT > 1) issue_half<false>(a.k_rsrc, lds.k[1], kTileKeys, wave, lane);
+  issue_half<true>(a.v_rsrc, lds.v[0], 0, wave, lane);
 
-  // K A-operand, key half kh, d chunk c: row 32kh + r32, logical 16-B chunk 2c + h.
+  // K A-operand, d chunk c: row r32 (+32 for the second key half, an immediate), logical 16-B
+  // chunk 2c + h.
 #pragma unroll
-  for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int row = 32 * kh + r32;
-      w.koff[kh][c] = row * kKRowBytes + (((2 * c + h) ^ swz_k(row)) << 4);
-    }
+  for (int c = 0; c < 4; ++c) w.koff[c] = r32 * kKRowBytes + (((2 * c + h) ^ swz_k(r32)) << 4);
   // V^T operand, d tile dt, run s of 4 keys: source lane (group g = lane/16, j = lane%16)
-  // reads V[16*c4 + 8s + 4(g/2) + j/4][32dt + 16(g%2) + 4(j%4) .. +3]; the c4 term is an
-  // immediate offset of 16 rows.
+  // reads V[16*cc + 8s + 4(g/2) + j/4][32dt + 16(g%2) + 4(j%4) .. +3]; the cc term and the key
+  // half are immediate offsets.
   {
     const int g = lane >> 4, jj = lane & 15;
 #pragma unroll
@@ -343,8 +441,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
       for (int sr = 0; sr < 2; ++sr) {
         const int row = 8 * sr + 4 * (g >> 1) + (jj >> 2);
         const int d0 = 32 * dt + 16 * (g & 1) + 4 * (jj & 3);
-        w.voff[dt][sr] = kHalfTileBytes + row * kKRowBytes + (((d0 >> 3) ^ swz_v(row)) << 4) +
-                         (d0 & 7) * 2;
+        w.voff[dt][sr] = row * kKRowBytes + (((d0 >> 3) ^ swz_v(row)) << 4) + (d0 & 7) * 2;
       }
   }
 #pragma unroll
@@ -355,15 +452,63 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
   w.m_run = -INFINITY;
   w.l_run = 0.f;
 
-  // Last visible key of this lane's row, for the element mask.
-  const int last_key = causal ? min(qrow, N - 1) : N - 1;
+  // Half-step 0 runs a P.V against V slot 2 with P = 0: zero that slot so no stale LDS value
+  // (possibly NaN) meets the zeros.
+  {
+    uint4* vz = reinterpret_cast<uint4*>(lds.v[2]);
+    vz[tid] = make_uint4(0u, 0u, 0u, 0u);
+    vz[tid + kThreads] = make_uint4(0u, 0u, 0u, 0u);
+  }
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc)
+    w.pb[cc] = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
 
-  for (int j = 0; j < nT; j += kStages) {
-    pipeline_step<0>(w, smem, j, nT, k_rsrc, v_rsrc, wave, lane, q0, N, causal, last_key, h, scale_log2);
-    if (j + 1 >= nT) break;
-    pipeline_step<1>(w, smem, j + 1, nT, k_rsrc, v_rsrc, wave, lane, q0, N, causal, last_key, h, scale_log2);
-    if (j + 2 >= nT) break;
-    pipeline_step<2>(w, smem, j + 2, nT, k_rsrc, v_rsrc, wave, lane, q0, N, causal, last_key, h, scale_log2);
+  // Wait for Q here, before the loop.  The compiler does not see the LDS transfers, so it
+  // places a full vmcnt(0) before this use of the Q registers; that also covers K_0, K_1 and V_0
+  // (once, in the prologue), and leaves no compiler-tracked loads whose waits could land inside
+  // the loop and drain the transfers in flight there.
+  asm volatile("" ::"v"(w.qop[0]), "v"(w.qop[1]), "v"(w.qop[2]), "v"(w.qop[3]));
+  wait_vmcnt<0>();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  lds_barrier();
+  if (a.nAct > 0) w.s = qk_half<0, 0>(w, lds);
+
+  // Steady tile steps: both half-steps full (2j + 1 < nAct).
+  const int nSteady = a.nAct / 2;
+  int j = 0;
+  for (; j + kStages <= nSteady; j += kStages) {
+    tile_step<0, true>(w, lds, j, a);
+    tile_step<1, true>(w, lds, j + 1, a);
+    tile_step<2, true>(w, lds, j + 2, a);
+  }
+  if (j < nSteady) {
+    tile_step<0, true>(w, lds, j, a);
+    ++j;
+    if (j < nSteady) {
+      tile_step<1, true>(w, lds, j, a);
+      ++j;
+    }
+  }
+  // Remaining tile steps (the wave's last half and P.V, then loads and barriers only).
+  for (; j < a.nT; ++j) {
+    const int sl = j % kStages;
+    if (sl == 0)
+      tile_step<0, false>(w, lds, j, a);
+    else if (sl == 1)
+      tile_step<1, false>(w, lds, j, a);
+    else
+      tile_step<2, false>(w, lds, j, a);
+  }
+  // P.V of the last computed half when it is the second half of the last tile (V_{nT-1}
+  // landed at the last step's barrier and its slot was not refilled): half-step 2nT.
+  if (a.nAct == 2 * a.nT) {
+    const int sl = (a.nT - 1) % kStages;
+    if (sl == 0)
+      pv_half<0, 1>(w, lds);
+    else if (sl == 1)
+      pv_half<1, 1>(w, lds);
+    else
+      pv_half<2, 1>(w, lds);
   }
 
   if (qrow < N) {
