@@ -117,6 +117,31 @@ def test_config_sampled_rows(name, nsample):
     assert np.all(np.abs(o) <= np.abs(v).max() + 1e-2)    # convex combination of V rows
 
 
+@pytest.mark.parametrize("name", ["config2", "config3", "config4"])
+def test_config_full_tensor_vs_reference_cpu_path(name):
+    """Every output element of configs 2-4 against the reference's own CPU attention path
+    (the fp32 "manual" branch, src/py/model_inference.py:68-75), one (batch, head) at a time."""
+    import torch as _t
+
+    from oracle import manual_attention_torch
+
+    cfg, q, k, v = _config_inputs(name)
+    _say(f"{name} full tensor vs CPU fp32 manual path")
+    o, lse = _run(q, k, v, cfg.scale, True)
+    _t.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    worst, total, count = 0.0, 0.0, 0
+    for b in range(cfg.B):
+        for hh in range(cfg.H):
+            ref = manual_attention_torch(_t.from_numpy(q[b:b + 1, hh:hh + 1]), _t.from_numpy(k[b:b + 1, hh:hh + 1]),
+                                         _t.from_numpy(v[b:b + 1, hh:hh + 1]))[0, 0].numpy()
+            d = np.abs(o[b, hh].astype(np.float64) - ref)
+            worst = max(worst, float(d.max()))
+            total += float(d.sum())
+            count += d.size
+    _say(f"{name} full: max|dO|={worst:.3e} mean|dO|={total / count:.3e}")
+    assert worst <= TOL_MAX and total / count <= TOL_MEAN
+
+
 # ------------------------------------------------------------------ reference test shapes
 
 

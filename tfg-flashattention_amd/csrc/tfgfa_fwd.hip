@@ -18,7 +18,7 @@
 //
 // Per-wave software pipeline (32-key halves u = 0, 1, ...)
 //   half-step u:  O += V_{u-1} P_{u-1}   together with   row max of S_u
-//                 (rescale O, l if the max moved: rare, lazy)
+//                 (rescale O, l if some row max moved: wave-uniform branch)
 //                 S_{u+1} = K_{u+1} Q^T  together with   P_u = exp2(S_u - m), l += rowsum
 //   Each MFMA group shares a basic block with VALU work that does not depend on it, so the
 //   MFMA pipe and the VALU stay busy at the same time; the S double buffer is 2 x 16
@@ -89,10 +89,12 @@ constexpr int kTileBytes = 2 * kHalfTileBytes;          // 16 KiB per stage
 constexpr int kStages = 3;
 constexpr int kLoadsPerWave = 2 * (kHalfTileBytes / 1024) / kWaves;  // 1 KiB per load instr: 4
 
-// The running max used as the exp2 offset is only moved when a row's tile max exceeds it by
-// more than this (log2 units), so most tiles skip the O/l rescale; probabilities then stay
-// below 2^8, well inside bf16/fp32 range.
-constexpr float kRescaleThreshold = 8.0f;
+// The exp2 offset is the exact running max of each row (moved whenever a half's max exceeds
+// it).  The row's largest score then gets probability exp2(0) = 1, which bf16 represents
+// exactly, so rounding P to bf16 for the MFMA leaves the dominant term of P.V exact; with a
+// lazier offset the dominant probability carries a 2^-9 relative error, which at GPT-2-XL
+// logit scales (sigma 3) costs up to ~1e-2 absolute in O.
+constexpr float kRescaleThreshold = 0.0f;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -262,9 +264,9 @@ __device__ __forceinline__ float row_max(const WaveState& w, float scale_log2) {
   return pair_max(mx) * scale_log2;
 }
 
-// Lazy rescale of O and l when the row max moved by more than the threshold.  Every computed
-// half has an unmasked key in every row (it starts at or below the wave's first row), so the
-// max is finite and the first half always moves m_run off -inf.
+// Rescale of O and l when some row's max moved (skipped, wave-uniformly, when none did).
+// Every computed half has an unmasked key in every row (it starts at or below the wave's first
+// row), so the max is finite and the first half always moves m_run off -inf.
 __device__ __forceinline__ void rescale(WaveState& w, float m_tile) {
   const bool grow = m_tile > w.m_run + kRescaleThreshold;
   if (__builtin_amdgcn_ballot_w64(grow) != 0) {
