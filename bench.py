@@ -43,6 +43,20 @@ def bytes_per_fwd(b=B, h=H, n=N, d=D):
     return 2.0 * 4 * b * h * n * d + 4.0 * b * h * n
 
 
+def committed_traffic():
+    """HBM bytes per launch measured by rocprofv3 (FETCH_SIZE and WRITE_SIZE, scaled by a copy
+    kernel of known size) for this workload, from the committed summary; None if absent."""
+    path = os.path.join(ROOT, "profiles", "fwd_kernel_config3_counters.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(gpu_o_sample, q_sample, k_sample, v_sample, heads_in_sample):
     """Times the reference's PyTorch CPU "manual" attention (fp32) on a sample of the
     workload: `heads_in_sample` (b, h) heads of input set 0 (all 200 by default, i.e. the
@@ -174,7 +188,8 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": committed_traffic(),
+            "traffic_source": "profiles/fwd_kernel_config3_counters.txt (rocprofv3 --pmc FETCH_SIZE x2.0 + WRITE_SIZE x1.0)",
             "algorithmic_bytes": bytes_per_fwd(),
             "hbm_GBps_at_algorithmic_bytes": round(bytes_per_fwd() / (ms * 1e-3) / 1e9, 1),
             "hbm_ceiling_frac_of_mfma_peak": round(
