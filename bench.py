@@ -12,7 +12,7 @@ Prints one JSON line.  ``value`` is TFLOP/s with the FlashAttention causal conve
 ``cpu_baseline`` times the reference's PyTorch CPU attention path (the "manual" branch of
 src/py/model_inference.py:68-75) on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 2000] [--no-cpu-baseline] [--no-strided]
 """
 import argparse
 import json
@@ -92,12 +92,57 @@ def cpu_baseline(gpu_o_sample, q_sample, k_sample, v_sample, heads_in_sample):
     }
 
 
+def time_strided_views(dev, steps, warmup):
+    """Same workload through tfgfa_fwd_bf16_strided with the operands of a GPT-2 block as they
+    come out of the Q/K/V projections: (B, N, H, 64) buffers read as (B, H, N, 64) views and O
+    written into a (B, N, H, 64) buffer (no copies before or after the kernel)."""
+    import torch
+
+    from custom_flash_attn import _C
+
+    gen = torch.Generator(device=dev).manual_seed(2003)
+    sets = []
+    for _ in range(N_SETS):
+        q, k, v = ((torch.randn(B, N, H, D, device=dev, generator=gen) * s).to(torch.bfloat16).transpose(1, 2)
+                   for s in (SIGMA_QK, SIGMA_QK, SIGMA_V))
+        o = torch.empty(B, N, H, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+        lse = torch.empty(B, H, N, device=dev, dtype=torch.float32)
+        sets.append((q, k, v, o, lse))
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def step(i):
+        q, k, v, o, lse = sets[i % N_SETS]
+        _C.fwd_strided(q.data_ptr(), q.stride(), k.data_ptr(), k.stride(), v.data_ptr(), v.stride(),
+                       o.data_ptr(), o.stride(), lse.data_ptr(), B, H, N, D, SCALE, True, sh)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    return {"layout": "q, k, v: (B, N, H, 64) buffers viewed (B, H, N, 64); o: (B, N, H, 64) buffer",
+            "ms_per_step": round(ms, 5), "value": round(flops_per_fwd() / (ms * 1e-3) / 1e12, 2),
+            "unit": "TFLOP/s", "steps": steps}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=200)
+    # Launch durations drift down for the first ~20-30 ms of back-to-back work while the GPU's
+    # clocks settle (a kernel trace of 700 launches shows ~60 us at the start, ~52 us after
+    # 300 launches), so the default warm-up is ~0.1 s of launches.
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-strided", action="store_true",
+                    help="skip the second timing of the same workload on strided (B, N, H, 64) views")
     ap.add_argument("--cpu-heads", type=int, default=200,
                     help="heads of the workload timed by the CPU baseline")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -197,6 +242,8 @@ def main():
         },
         "device": info,
     }
+    if not args.no_strided:
+        result["strided_gpt2_views"] = time_strided_views(dev, max(1, args.steps // 2), max(1, args.warmup // 2))
     if not args.no_cpu_baseline:
         nh = max(1, min(args.cpu_heads, B * H))
         q, k, v, o = (t.reshape(1, B * H, N, D)[:, :nh] for t in sets[0][:4])

@@ -14,9 +14,11 @@
  * FFI (pybind11, ctypes, cgo ...) can bind it.
  *
  * Conventions shared by every entry point:
- *  - Q, K, V, O are contiguous (B, H, N, D) bfloat16 tensors in device memory
- *    (strides H*N*D, N*D, D, 1), 16-byte aligned.  This is the layout
- *    torch_bind.cpp:27-31 assumes (size(0..2) read as B, H, N; O = empty_like(Q)).
+ *  - Q, K, V, O are (B, H, N, D) bfloat16 tensors in device memory, 16-byte
+ *    aligned.  tfgfa_fwd_bf16 takes them contiguous (strides H*N*D, N*D, D, 1),
+ *    the layout torch_bind.cpp:27-31 assumes (size(0..2) read as B, H, N;
+ *    O = empty_like(Q)); tfgfa_fwd_bf16_strided takes any strides that keep
+ *    the last dimension dense.
  *  - LSE, when requested, is a contiguous (B, H, N) float32 tensor holding the
  *    natural-log log-sum-exp of each row's scaled, masked scores:
  *        LSE[b,h,i] = log( sum_{j <= i} exp(scale * q_i . k_j) )
@@ -31,11 +33,13 @@
 #ifndef TFGFA_H
 #define TFGFA_H
 
+#include <stdint.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-#define TFGFA_ABI_VERSION 1
+#define TFGFA_ABI_VERSION 2
 
 /* Status codes (> 0: invalid argument). */
 #define TFGFA_OK                 0
@@ -46,6 +50,7 @@ extern "C" {
 #define TFGFA_ERR_CAUSAL_FLAG    5  /* causal is neither 0 nor 1                     */
 #define TFGFA_ERR_TOO_LARGE      6  /* grid or element count exceeds the limits      */
 #define TFGFA_ERR_ALIGNMENT      7  /* q/k/v/o not 16-byte aligned or lse not 4-byte */
+#define TFGFA_ERR_STRIDE         8  /* strides outside what tfgfa_fwd_bf16_strided takes */
 
 /*
  * Attention forward, bf16 in / bf16 out, fp32 accumulation and softmax.
@@ -65,6 +70,32 @@ extern "C" {
 int tfgfa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
                    int B, int H, int N, int D, float softmax_scale, int causal,
                    void* hip_stream);
+
+/*
+ * The same attention over strided operands: each of q, k, v, o is described by
+ * its base pointer and four element strides (batch, head, row, dim), as
+ * torch's Tensor.stride() gives them; a NULL strides pointer means contiguous.
+ * This lets a caller pass the (B, N, H, D) projections of a GPT-2 block as
+ * (B, H, N, D) views (strides N*H*D, D, H*D, 1) and have O written straight
+ * into a (B, N, H, D) buffer, so neither side needs a transposing copy
+ * (the reference's caller views and transposes, src/py/model_inference.py:64-66,
+ * copies Q, K, V with .contiguous(), :86-90, and O again, :92).
+ * Rules (TFGFA_ERR_STRIDE otherwise): dim stride 1; batch, head and row strides
+ * non-negative multiples of 8; row stride >= 64; no two elements of O at one
+ * address (checked: sorted by stride, each stride of a dimension of size > 1
+ * exceeds the span of the smaller ones).  The stride of a dimension of size 1
+ * is ignored.  (N + 128) * row stride * 2 must be < 2^31 (TFGFA_ERR_TOO_LARGE).
+ * O must not overlap K or V (not checked).
+ * LSE, when requested, stays a contiguous (B, H, N) float32 tensor.
+ * No counterpart in the reference's C++ (its binding requires contiguous
+ * tensors, torch_bind.cpp:14-16); it replaces the copies its caller makes.
+ */
+int tfgfa_fwd_bf16_strided(const void* q, const int64_t* q_strides,
+                           const void* k, const int64_t* k_strides,
+                           const void* v, const int64_t* v_strides,
+                           void* o, const int64_t* o_strides, float* lse,
+                           int B, int H, int N, int D, float softmax_scale, int causal,
+                           void* hip_stream);
 
 /*
  * Human-readable text for a status code returned by any tfgfa_* function.

@@ -33,6 +33,9 @@ def lib():
     lib.tfgfa_fwd_bf16.restype = ctypes.c_int
     lib.tfgfa_fwd_bf16.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_void_p] + [ctypes.c_int] * 4 + [
         ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
+    lib.tfgfa_fwd_bf16_strided.restype = ctypes.c_int
+    lib.tfgfa_fwd_bf16_strided.argtypes = [ctypes.c_void_p, ctypes.c_void_p] * 4 + [ctypes.c_void_p] + [
+        ctypes.c_int] * 4 + [ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
     lib.tfgfa_strerror.restype = ctypes.c_char_p
     lib.tfgfa_strerror.argtypes = [ctypes.c_int]
     lib.tfgfa_abi_version.restype = ctypes.c_int
@@ -41,7 +44,8 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     names = _header_functions()
-    assert names == ["tfgfa_abi_version", "tfgfa_device_info", "tfgfa_fwd_bf16", "tfgfa_strerror"]
+    assert names == ["tfgfa_abi_version", "tfgfa_device_info", "tfgfa_fwd_bf16",
+                     "tfgfa_fwd_bf16_strided", "tfgfa_strerror"]
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/tfgfa.h but not exported"
 
@@ -54,7 +58,8 @@ def test_abi_version(lib):
 def test_strerror_covers_every_status(lib):
     codes = [_header_define(n) for n in (
         "TFGFA_OK", "TFGFA_ERR_NULL_POINTER", "TFGFA_ERR_BAD_SHAPE", "TFGFA_ERR_HEAD_DIM",
-        "TFGFA_ERR_SCALE", "TFGFA_ERR_CAUSAL_FLAG", "TFGFA_ERR_TOO_LARGE", "TFGFA_ERR_ALIGNMENT")]
+        "TFGFA_ERR_SCALE", "TFGFA_ERR_CAUSAL_FLAG", "TFGFA_ERR_TOO_LARGE", "TFGFA_ERR_ALIGNMENT",
+        "TFGFA_ERR_STRIDE")]
     msgs = [lib.tfgfa_strerror(c).decode() for c in codes]
     assert len(set(msgs)) == len(msgs)
     assert lib.tfgfa_strerror(12345).decode() == "unknown tfgfa status"
@@ -91,6 +96,82 @@ def test_c_abi_argument_validation(lib, args, code):
     assert lib.tfgfa_fwd_bf16(*args, None) == _header_define(code)
 
 
+def _st(*vals):
+    return (ctypes.c_int64 * 4)(*vals)
+
+
+def _contig(B, H, N):
+    return _st(H * N * 64, N * 64, 64, 1)
+
+
+# Strided entry point.  Strides are checked before pointers, so a NULL-pointer status means the
+# strides were accepted; no case here reaches a launch.
+@pytest.mark.parametrize("B,H,N,qs,code", [
+    (2, 3, 16, None, "TFGFA_ERR_NULL_POINTER"),                        # NULL strides: contiguous
+    (2, 3, 16, (3 * 16 * 64, 16 * 64, 64, 1), "TFGFA_ERR_NULL_POINTER"),
+    (2, 3, 16, (16 * 3 * 64, 64, 3 * 64, 1), "TFGFA_ERR_NULL_POINTER"),  # (B, N, H, D) view
+    (2, 3, 16, (16 * 9 * 64, 64, 9 * 64, 1), "TFGFA_ERR_NULL_POINTER"),  # fused QKV rows
+    (2, 3, 16, (3 * 16 * 72, 16 * 72, 72, 1), "TFGFA_ERR_NULL_POINTER"),  # padded rows
+    (1, 1, 16, (7, 3, 64, 1), "TFGFA_ERR_NULL_POINTER"),                # size-1 dims ignored
+    (2, 3, 1, (3 * 64, 64, 5, 1), "TFGFA_ERR_NULL_POINTER"),            # N = 1: row stride ignored
+    (2, 3, 16, (3 * 16 * 64, 16 * 64, 64, 2), "TFGFA_ERR_STRIDE"),      # dim not dense
+    (2, 3, 16, (3 * 16 * 64, 16 * 64, 32, 1), "TFGFA_ERR_STRIDE"),      # overlapping rows
+    (2, 3, 16, (3 * 16 * 64, 16 * 64, 0, 1), "TFGFA_ERR_STRIDE"),
+    (2, 3, 16, (3 * 16 * 64, 16 * 64, 68, 1), "TFGFA_ERR_STRIDE"),      # 136 B rows: misaligned
+    (2, 3, 16, (3 * 16 * 64, 16 * 64 + 4, 64, 1), "TFGFA_ERR_STRIDE"),
+    (2, 3, 16, (3 * 16 * 64 + 4, 16 * 64, 64, 1), "TFGFA_ERR_STRIDE"),
+    (2, 3, 16, (-3 * 16 * 64, 16 * 64, 64, 1), "TFGFA_ERR_STRIDE"),
+    (2, 3, 16, (3 * 16 * 64, -16 * 64, 64, 1), "TFGFA_ERR_STRIDE"),
+    (2, 3, 16, (0, 0, 1 << 30, 1), "TFGFA_ERR_TOO_LARGE"),              # 32-bit buffer offsets
+    (2, 3, 4096, (0, 0, (1 << 18), 1), "TFGFA_ERR_TOO_LARGE"),
+    (0, 3, 16, (0, 0, 1, 5), "TFGFA_OK"),                               # empty: nothing checked
+])
+@pytest.mark.parametrize("which", [0, 1, 2, 3])
+def test_c_abi_strided_validation(lib, B, H, N, qs, code, which):
+    strides = [_contig(B, H, N) for _ in range(4)]
+    strides[which] = None if qs is None else _st(*qs)
+    args = []
+    for s in strides:
+        args += [None, s]
+    assert lib.tfgfa_fwd_bf16_strided(*args, None, B, H, N, 64, 0.125, 1, None) == _header_define(code)
+
+
+@pytest.mark.parametrize("os_,code", [
+    ((0, 0, 64, 1), "TFGFA_ERR_STRIDE"),                    # every head onto one
+    ((3 * 16 * 64, 0, 64, 1), "TFGFA_ERR_STRIDE"),
+    ((3 * 16 * 64, 64, 64, 1), "TFGFA_ERR_STRIDE"),         # heads and rows collide
+    ((3 * 16 * 64, 16 * 64 - 8, 64, 1), "TFGFA_ERR_STRIDE"),  # last row of a head hits the next
+    ((16 * 3 * 64, 64, 3 * 64, 1), "TFGFA_ERR_NULL_POINTER"),  # (B, N, H, D) buffer
+    ((64, 2 * 64, 6 * 64, 1), "TFGFA_ERR_NULL_POINTER"),     # batch innermost
+    ((3 * 16 * 80, 16 * 80, 80, 1), "TFGFA_ERR_NULL_POINTER"),  # padded rows
+])
+def test_c_abi_strided_output_overlap(lib, os_, code):
+    B, H, N = 2, 3, 16
+    c = _contig(B, H, N)
+    assert lib.tfgfa_fwd_bf16_strided(None, c, None, c, None, c, None, _st(*os_), None,
+                                      B, H, N, 64, 0.125, 1, None) == _header_define(code)
+    # Inputs may share elements (e.g. K broadcast over heads).
+    assert lib.tfgfa_fwd_bf16_strided(None, _st(*os_), None, c, None, c, None, c, None,
+                                      B, H, N, 64, 0.125, 1, None) == _header_define("TFGFA_ERR_NULL_POINTER")
+
+
+def test_c_abi_strided_checks_sizes_before_strides(lib):
+    bad = _st(0, 0, 1, 5)
+    assert lib.tfgfa_fwd_bf16_strided(None, bad, None, bad, None, bad, None, bad, None,
+                                      1, 1, 16, 128, 0.125, 1, None) == _header_define("TFGFA_ERR_HEAD_DIM")
+    ok = _contig(1, 1, 16)
+    assert lib.tfgfa_fwd_bf16_strided(P + 2, ok, P, ok, P, ok, P, ok, None,
+                                      1, 1, 16, 64, 0.125, 1, None) == _header_define("TFGFA_ERR_ALIGNMENT")
+
+
+def test_pybind_strided_raises_runtime_error_with_message():
+    c = (64 * 16, 64 * 16, 64, 1)
+    with pytest.raises(RuntimeError, match="unsupported strides"):
+        _C.fwd_strided(P, (64 * 16, 64 * 16, 32, 1), P, c, P, c, P, c, 0, 1, 1, 16, 64, 0.125, True, 0)
+    with pytest.raises(RuntimeError, match="tfgfa_fwd_bf16_strided failed"):
+        _C.fwd_strided(0, c, P, c, P, c, P, c, 0, 1, 1, 16, 64, 0.125, True, 0)
+
+
 def test_pybind_raises_runtime_error_with_message():
     with pytest.raises(RuntimeError, match="unsupported head dimension"):
         _C.fwd(P, P, P, P, 0, 1, 1, 16, 128, 0.125, True, 0)
@@ -112,12 +193,18 @@ def test_forward_rejects_cpu_tensors_like_the_reference():
 class _FakeCuda:
     """Stands in for a device tensor so the shim's later checks can run on the CPU."""
 
-    def __init__(self, shape=(1, 2, 8, 64), dtype=torch.bfloat16, contiguous=True, device="cuda:0"):
+    def __init__(self, shape=(1, 2, 8, 64), dtype=torch.bfloat16, contiguous=True, device="cuda:0",
+                 last_stride=1):
         self.shape = torch.Size(shape)
         self.dtype = dtype
         self.is_cuda = True
         self._contig = contiguous
         self.device = torch.device(device)
+        self._last_stride = last_stride
+
+    def stride(self, dim=None):
+        st = (0, 0, 0, self._last_stride)[-len(self.shape):]
+        return st if dim is None else st[dim]
 
     def is_contiguous(self):
         return self._contig
@@ -141,6 +228,32 @@ class _FakeCuda:
 def test_shim_validation_messages(qkv, msg):
     with pytest.raises(RuntimeError, match=msg):
         custom_flash_attn._validate(*qkv)
+
+
+@pytest.mark.parametrize("qkv,out,msg", [
+    ((_FakeCuda(dtype=torch.float16), _FakeCuda(), _FakeCuda()), None, r"^Unsupported tensor dtype"),
+    ((_FakeCuda(shape=(2, 8, 64)),) * 3, None, "q must be 4-D"),
+    ((_FakeCuda(), _FakeCuda(shape=(1, 2, 9, 64)), _FakeCuda()), None, "k must have shape"),
+    ((_FakeCuda(), _FakeCuda(), _FakeCuda(device="cuda:1")), None, "v must be on"),
+    ((_FakeCuda(shape=(1, 2, 8, 128)),) * 3, None, "head_dim must be 64"),
+    ((_FakeCuda(), _FakeCuda(last_stride=2), _FakeCuda()), None, r"k must be dense in its last dimension"),
+    ((_FakeCuda(),) * 3, _FakeCuda(shape=(1, 2, 8, 32)), "out must have shape"),
+    ((_FakeCuda(),) * 3, _FakeCuda(dtype=torch.float32), r"^Unsupported tensor dtype"),
+])
+def test_attention_view_validation_messages(qkv, out, msg):
+    # Non-contiguous views are accepted: only the last dimension must be dense.
+    with pytest.raises(RuntimeError, match=msg):
+        custom_flash_attn._check_view(qkv[0], "q", None)
+        custom_flash_attn._check_view(qkv[1], "k", qkv[0])
+        custom_flash_attn._check_view(qkv[2], "v", qkv[0])
+        if out is not None:
+            custom_flash_attn._check_view(out, "out", qkv[0])
+
+
+def test_attention_rejects_cpu_tensors():
+    q = torch.zeros(1, 1, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="^q must be a CUDA tensor$"):
+        custom_flash_attn.attention(q, q, q)
 
 
 def test_forward_is_positional_only():

@@ -12,7 +12,9 @@ the bf16 Q/K/V/out projections.  The noise floor is measured by a control run on
 whose attention is computed in fp32 from the same bf16 Q/K/V (and rounded to bf16 like the
 kernel's output).  The kernel run must stay within 1.5x the control's relative L2 error
 (plus 1e-4), its relative L2 error must be below 2e-2, and the argmax agreement with the
-CPU logits must be at least 0.97x the control's.
+CPU logits must be at least 0.97x the control's.  The "hip" (strided, copy-free) and
+"cuda" (contiguous copies, as the reference calls the kernel) branches run the same kernel on
+the same values, so their logits must be bit-identical.
 """
 import math
 import sys
@@ -69,44 +71,48 @@ def test_gpt2_medium_logits_match_cpu(gpt2_medium_cpu_reference):
     try:
         gpu = model.to("cuda:0")
         idx_d = idx.to("cuda:0")
-        results = {}
-        for impl in ("hip", "fp32_control"):
+        results, logits = {}, {}
+        for impl in ("hip", "cuda", "fp32_control"):
             for blk in gpu.trf_blocks:
                 blk.att.impl_type = impl
             _say(f"config5: GPU forward impl={impl}")
             with torch.no_grad():
                 out = gpu(idx_d).float().cpu()
             torch.cuda.synchronize()
+            logits[impl] = out
             results[impl] = _stats(out, ref)
             _say(f"config5 {impl}: rel_l2={results[impl][0]:.3e} max_abs={results[impl][1]:.3e} "
                  f"argmax_agree={results[impl][2]:.4f}")
     finally:
         del mi.ATTENTION_IMPLS["fp32_control"]
         model.to("cpu")
+    assert torch.equal(logits["hip"], logits["cuda"]), "strided and contiguous branches differ"
     hip, ctl = results["hip"], results["fp32_control"]
     assert hip[0] <= 1.5 * ctl[0] + 1e-4
     assert hip[0] < 2e-2
     assert hip[2] >= 0.97 * ctl[2]
 
 
-def test_hip_attention_is_the_kernel(monkeypatch):
-    """The "hip" branch must reach custom_flash_attn.forward (no silent fallback)."""
+@pytest.mark.parametrize("impl,entry", [("hip", "attention"), ("cuda", "forward")])
+def test_hip_attention_is_the_kernel(monkeypatch, impl, entry):
+    """Both kernel branches must reach the native entry points (no silent fallback); the
+    "hip" branch hands the kernel non-contiguous views and gets no copy back."""
     import custom_flash_attn
 
     calls = []
-    real = custom_flash_attn.forward
+    real = getattr(custom_flash_attn, entry)
 
-    def spy(q, k, v):
-        calls.append(q.shape)
-        return real(q, k, v)
+    def spy(q, k, v, **kw):
+        calls.append((q.shape, q.is_contiguous()))
+        return real(q, k, v, **kw)
 
-    monkeypatch.setattr(custom_flash_attn, "forward", spy)
+    monkeypatch.setattr(custom_flash_attn, entry, spy)
     cfg = dict(mi.GPT_CONFIG_124M)
     cfg.update({"emb_dim": 256, "n_layers": 2, "n_heads": 4, "vocab_size": 101,
-                "context_length": 128, "drop_rate": 0.0, "qkv_bias": True, "impl_type": "hip"})
+                "context_length": 128, "drop_rate": 0.0, "qkv_bias": True, "impl_type": impl})
     model = mi.GPTModel(cfg).eval().to("cuda:0")
     mi.init_gpt2_weights(model, 1)
     with torch.no_grad():
         out = model(torch.randint(0, 101, (2, 100), device="cuda:0"))
     assert out.shape == (2, 100, 101) and torch.isfinite(out).all()
-    assert calls == [torch.Size([2, 4, 100, 64])] * 2
+    assert calls == [(torch.Size([2, 4, 100, 64]), impl == "cuda")] * 2

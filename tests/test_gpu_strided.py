@@ -1,0 +1,152 @@
+"""Strided operands through tfgfa_fwd_bf16_strided (GPU box only).
+
+The kernel's arithmetic does not depend on where rows live, so every strided call is
+checked bit-for-bit against the contiguous entry point on the same values, and once
+against the CPU oracle (tolerances as in test_gpu_parity.py: max|dO| <= 2e-2,
+mean|dO| <= 2e-3, max|dLSE| <= 1e-3).  Output buffers are filled with a sentinel first:
+elements that are not part of O (padding between rows, heads or batches) must keep it.
+Inputs follow the BASELINE configs' distributions (Q, K ~ N(0, 2^2..3^2), V ~ N(0, 1)),
+the distributions the tolerances are stated for: O's error scales with |V|.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_c
+
+import custom_flash_attn
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TOL_MAX, TOL_MEAN, TOL_LSE = 2e-2, 2e-3, 1e-3
+SENTINEL = -12345.0  # exactly representable in bf16
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _randn(shape, seed, sigma=1.0):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return (torch.randn(shape, device=DEV, generator=g) * sigma).to(torch.bfloat16)
+
+
+def _contiguous_ref(q, k, v, scale=None, causal=True):
+    o, lse = custom_flash_attn.forward_lse(q.contiguous(), k.contiguous(), v.contiguous(),
+                                           softmax_scale=scale, causal=causal)
+    return o, lse
+
+
+def _assert_same(o, lse, o_ref, lse_ref, label):
+    torch.cuda.synchronize()
+    assert torch.equal(o.contiguous().view(torch.int16), o_ref.view(torch.int16)), f"{label}: O differs"
+    if lse is not None:
+        assert torch.equal(lse, lse_ref), f"{label}: LSE differs"
+
+
+def _oracle_check(o, lse, q, k, v, scale, causal, label):
+    qn, kn, vn = (t.float().contiguous().cpu().numpy() for t in (q, k, v))
+    o_ref, lse_ref = attention_c(qn, kn, vn, scale, causal)
+    d = np.abs(o.float().cpu().numpy().astype(np.float64) - o_ref)
+    dl = np.abs(lse.cpu().numpy().astype(np.float64) - lse_ref)
+    _say(f"{label}: max|dO|={d.max():.3e} mean|dO|={d.mean():.3e} max|dLSE|={dl.max():.3e}")
+    assert d.max() <= TOL_MAX and d.mean() <= TOL_MEAN and dl.max() <= TOL_LSE, label
+
+
+@pytest.mark.parametrize("B,H,N", [(2, 4, 256), (1, 3, 1000), (3, 2, 65), (2, 2, 1)])
+def test_gpt2_projection_views(B, H, N):
+    """Q, K, V as (B, N, H, 64) projections viewed (B, H, N, 64); O written into a
+    (B, N, H, 64) buffer through its transposed view."""
+    _say(f"gpt2 views B={B} H={H} N={N}")
+    D = 64
+    x = _randn((3, B, N, H * D), seed=11 + N, sigma=2.0)
+    x[2].mul_(0.5)  # V ~ N(0, 1) (exact in bf16)
+    q, k, v = (x[i].view(B, N, H, D).transpose(1, 2) for i in range(3))
+    assert not q.is_contiguous() or N == 1
+    buf = torch.empty(B, N, H, D, device=DEV, dtype=torch.bfloat16)
+    out, lse = custom_flash_attn.attention(q, k, v, out=buf.transpose(1, 2), return_lse=True)
+    assert out.data_ptr() == buf.data_ptr()
+    o_ref, lse_ref = _contiguous_ref(q, k, v)
+    _assert_same(out, lse, o_ref, lse_ref, "gpt2 views")
+    if N >= 65:
+        _oracle_check(out, lse, q, k, v, 0.125, True, f"gpt2 views B={B} H={H} N={N} vs oracle")
+
+
+def test_fused_qkv_buffer_and_padded_output():
+    """Q, K, V interleaved in one (B, N, 3, H, 64) buffer (row stride 3*H*64), O into a
+    buffer with padded rows and heads; the padding keeps its sentinel."""
+    B, H, N, D = 2, 3, 300, 64
+    _say(f"fused qkv B={B} H={H} N={N}")
+    qkv = _randn((B, N, 3, H, D), seed=5, sigma=3.0)
+    qkv[:, :, 2].div_(3.0)  # V ~ N(0, 1)
+    q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+    big = torch.full((B, H + 1, N, D + 16), SENTINEL, device=DEV, dtype=torch.bfloat16)
+    out_view = big[:, :H, :, :D]
+    assert out_view.stride() == ((H + 1) * N * (D + 16), N * (D + 16), D + 16, 1)
+    out, lse = custom_flash_attn.attention(q, k, v, out=out_view, return_lse=True)
+    o_ref, lse_ref = _contiguous_ref(q, k, v)
+    _assert_same(out, lse, o_ref, lse_ref, "fused qkv")
+    assert (big[:, :H, :, D:] == SENTINEL).all(), "row padding written"
+    assert (big[:, H:] == SENTINEL).all(), "head padding written"
+    _oracle_check(out, lse, q, k, v, 0.125, True, "fused qkv vs oracle")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_distinct_strides_per_operand(causal):
+    """Each operand in its own layout: Q contiguous, K rows padded to 72, V (N, B, H, 64)
+    order, O head-major with padded batches."""
+    B, H, N, D = 2, 2, 333, 64
+    _say(f"distinct strides causal={causal}")
+    q = _randn((B, H, N, D), seed=21, sigma=3.0)
+    kbig = _randn((B, H, N, 72), seed=22, sigma=3.0)
+    k = kbig[..., :D]
+    vbig = _randn((N, B, H, D), seed=23)
+    v = vbig.permute(1, 2, 0, 3)
+    obig = torch.full((H, B + 1, N, D), SENTINEL, device=DEV, dtype=torch.bfloat16)
+    o = obig[:, :B].transpose(0, 1)
+    out, lse = custom_flash_attn.attention(q, k, v, out=o, causal=causal, return_lse=True)
+    o_ref, lse_ref = _contiguous_ref(q, k, v, causal=causal)
+    _assert_same(out, lse, o_ref, lse_ref, "distinct strides")
+    assert (obig[:, B:] == SENTINEL).all()
+    _oracle_check(out, lse, q, k, v, 0.125, causal, f"distinct strides causal={causal} vs oracle")
+
+
+def test_size_one_dims_with_unusual_strides():
+    """B = H = 1 views whose batch/head strides are meaningless (torch allows any)."""
+    N, D = 200, 64
+    base = _randn((N, 1, 1, D), seed=31, sigma=3.0)
+    q = base.as_strided((1, 1, N, D), (7, 3, D, 1))
+    k = _randn((1, 1, N, D), seed=32, sigma=3.0)
+    v = _randn((1, 1, N, D), seed=33)
+    out = custom_flash_attn.attention(q, k, v)
+    o_ref, _ = _contiguous_ref(q, k, v)
+    _assert_same(out, None, o_ref, None, "size-one dims")
+
+
+def test_strided_no_lse_and_default_out_is_contiguous():
+    B, H, N, D = 1, 2, 129, 64
+    x = _randn((B, N, 3 * H * D), seed=41, sigma=2.0)
+    q, k, v = (x[..., i * H * D:(i + 1) * H * D].view(B, N, H, D).transpose(1, 2) for i in range(3))
+    out = custom_flash_attn.attention(q, k, v, softmax_scale=0.3)
+    assert out.is_contiguous() and out.shape == (B, H, N, D)
+    o_ref, _ = _contiguous_ref(q, k, v, scale=0.3)
+    _assert_same(out, None, o_ref, None, "no lse")
+
+
+def test_rejected_layouts_raise_before_launch():
+    B, H, N, D = 1, 2, 64, 64
+    x = _randn((B, H, N, 2 * D), seed=51)
+    with pytest.raises(RuntimeError, match="stride 1"):
+        custom_flash_attn.attention(x[..., ::2], x[..., ::2], x[..., ::2])
+    y = _randn((B, H, N * 64 + 4), seed=52).as_strided((B, H, N, D), (H * (N * 64 + 4), N * 64 + 4, 64, 1),
+                                                        storage_offset=4)
+    with pytest.raises(RuntimeError, match="unsupported strides|misaligned"):
+        custom_flash_attn.attention(y, y, y)
+    overlap = _randn((B, H, N + 1, 32), seed=53).view(-1)[: B * H * (N * 32 + 32)]
+    rows = overlap.as_strided((B, H, N, D), (H * (N + 1) * 32, (N + 1) * 32, 32, 1))
+    with pytest.raises(RuntimeError, match="unsupported strides"):
+        custom_flash_attn.attention(rows, rows, rows)

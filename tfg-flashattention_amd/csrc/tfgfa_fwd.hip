@@ -120,20 +120,21 @@ __device__ __forceinline__ float pair_sum(float x) {
 __device__ __forceinline__ int swz_k(int row) { return (row ^ ((row >> 3) & 3)) & 7; }
 __device__ __forceinline__ int swz_v(int row) { return (row & 3) << 1; }
 
-// Buffer descriptor over one head's (N, 64) bf16 rows, as four SGPRs for the loads issued from
-// inline assembly: base address, stride 0, num_records = N * 128 bytes, format word 0x20000
+// Buffer descriptor over one head's N rows of 64 bf16 (row r at byte r * row_bytes; row_bytes =
+// 128 for a contiguous head), as four SGPRs for the loads issued from inline assembly: base
+// address, stride 0, num_records = N * row_bytes, format word 0x20000
 // (the layout __builtin_amdgcn_make_buffer_rsrc builds for the Q loads).  A raw buffer load whose
 // byte offset is at or past num_records returns zero: that is the zero-fill of tiles and query
-// blocks past the sequence end.  The whole offset is kept in the VGPR operand so the range
+// blocks past the sequence end (row N starts exactly at num_records; row_bytes >= 128).  The whole offset is kept in the VGPR operand so the range
 // check covers all of it.
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ i32x4 head_desc(const __bf16* base, int N) {
+__device__ __forceinline__ i32x4 head_desc(const __bf16* base, int N, int row_bytes) {
   const uint64_t b = reinterpret_cast<uint64_t>(base);
   i32x4 d;
   d[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
   d[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
-  d[2] = N * kKRowBytes;
+  d[2] = N * row_bytes;
   d[3] = 0x00020000;
   return d;
 }
@@ -160,15 +161,18 @@ __device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
 // Lane i of a block fills physical chunk i%8 of row i/8, so it fetches the logical chunk that
 // the swizzle maps there.
 template <bool kIsV>
-__device__ __forceinline__ void issue_half(i32x4 desc, unsigned char* dst, int k0, int wave,
-                                           int lane) {
+__device__ __forceinline__ void issue_half(i32x4 desc, int row_bytes, unsigned char* dst, int k0,
+                                           int wave, int lane) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int blk = 2 * wave + i;
     const int row = blk * 8 + (lane >> 3);
     const int pc = lane & 7;
     const int sw = kIsV ? swz_v(row) : swz_k(row);
-    lds_transfer(desc, lds_addr(dst + blk * 1024), (k0 + row) * kKRowBytes + ((pc ^ sw) << 4));
+    // Uniform part (first row of the block) in a scalar register, per-lane part in a vector one.
+    const int s_off = __builtin_amdgcn_readfirstlane((k0 + blk * 8) * row_bytes);
+    lds_transfer(desc, lds_addr(dst + blk * 1024),
+                 s_off + ((lane >> 3) * row_bytes + ((pc ^ sw) << 4)));
   }
 }
 
@@ -305,6 +309,7 @@ __device__ __forceinline__ void exp_half(WaveState& w, float scale_log2) {
 // Loop-invariant inputs of the pipeline.
 struct StepArgs {
   i32x4 k_rsrc, v_rsrc;
+  int k_row_bytes, v_row_bytes;  // byte distance between consecutive K (V) rows of a head
   int nT;        // 64-key tiles loaded by the workgroup
   int nAct;      // 32-key halves this wave computes (a prefix)
   int nFull;     // halves this wave computes without an element mask (a prefix of the above)
@@ -342,8 +347,10 @@ __device__ __forceinline__ void tile_step(WaveState& w, const Lds& lds, int j,
   constexpr int kNext2 = (kSlot + 2) % kStages;
   constexpr int kPrev = (kSlot + kStages - 1) % kStages;
   const bool k2 = j + 2 < a.nT, v1 = j + 1 < a.nT;
-  if (k2) issue_half<false>(a.k_rsrc, lds.k[kNext2], (j + 2) * kTileKeys, a.wave, a.lane);
-  if (v1) issue_half<true>(a.v_rsrc, lds.v[kNext], (j + 1) * kTileKeys, a.wave, a.lane);
+  if (k2)
+    issue_half<false>(a.k_rsrc, a.k_row_bytes, lds.k[kNext2], (j + 2) * kTileKeys, a.wave, a.lane);
+  if (v1)
+    issue_half<true>(a.v_rsrc, a.v_row_bytes, lds.v[kNext], (j + 1) * kTileKeys, a.wave, a.lane);
   // Half 2j: P.V of half 2j-1 (V_{j-1}, keys 32..63), S of half 2j+1 (K_j, keys 32..63).
   half_step<kPrev, 1, kSlot, 1, kSteady>(w, lds, 2 * j, a);
   // K_{j+1} and V_j were issued by step j-1; only this step's loads may still be in flight.
@@ -358,10 +365,18 @@ __device__ __forceinline__ void tile_step(WaveState& w, const Lds& lds, int j,
   half_step<kSlot, 0, kNext, 0, kSteady>(w, lds, 2 * j + 1, a);
 }
 
+// Element strides of one (B, H, N, 64) operand: batch, head, row (the last dim is contiguous).
+struct Strides {
+  long long b, h, n;
+};
+
+// kDense: every operand is the contiguous (B, H, N, 64) layout, so row strides are the
+// compile-time 128 B and the stride arguments are not read (the tfgfa_fwd_bf16 case).
+template <bool kDense>
 __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
     const __bf16* __restrict__ Q, const __bf16* __restrict__ K, const __bf16* __restrict__ V,
-    __bf16* __restrict__ O, float* __restrict__ LSE, int BH, int N, int nQB, float scale_log2,
-    int causal) {
+    __bf16* __restrict__ O, float* __restrict__ LSE, int H, int BH, int N, int nQB,
+    float scale_log2, int causal, Strides qs, Strides ks, Strides vs, Strides os) {
   __shared__ __attribute__((aligned(1024))) unsigned char k0s[kHalfTileBytes];
   __shared__ __attribute__((aligned(1024))) unsigned char k1s[kHalfTileBytes];
   __shared__ __attribute__((aligned(1024))) unsigned char k2s[kHalfTileBytes];
@@ -383,11 +398,16 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
   const int qb = nQB - 1 - bid / BH;
   const int bh = bid % BH;
 
-  const size_t head_off = (size_t)bh * N * kD;
+  const int bb = bh / H, hh = bh - bb * H;
+  const long long dense_head = (long long)bh * N * kD;
+  const __bf16* Qh = kDense ? Q + dense_head : Q + bb * qs.b + hh * qs.h;
+  const int q_row_bytes = kDense ? kKRowBytes : (int)qs.n * 2;
 
   StepArgs a;
-  a.k_rsrc = head_desc(K + head_off, N);
-  a.v_rsrc = head_desc(V + head_off, N);
+  a.k_row_bytes = kDense ? kKRowBytes : (int)ks.n * 2;
+  a.v_row_bytes = kDense ? kKRowBytes : (int)vs.n * 2;
+  a.k_rsrc = head_desc(kDense ? K + dense_head : K + bb * ks.b + hh * ks.h, N, a.k_row_bytes);
+  a.v_rsrc = head_desc(kDense ? V + dense_head : V + bb * vs.b + hh * vs.h, N, a.v_row_bytes);
   const int q0 = qb * kBlockRows + wave * kWaveRows;  // first query row of this wave
   const int qrow = q0 + r32;                          // this lane's query row
   const int kv_end = causal ? min(N, (qb + 1) * kBlockRows) : N;
@@ -418,15 +438,15 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
   WaveState w;
   {
     const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<__bf16*>(Q + head_off), (short)0, N * kKRowBytes, 0x00020000);
+        const_cast<__bf16*>(Qh), (short)0, N * q_row_bytes, 0x00020000);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       w.qop[c] = __builtin_bit_cast(
-          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(qr, qrow * kKRowBytes + 32 * c + 16 * h, 0, 0));
+          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(qr, qrow * q_row_bytes + 32 * c + 16 * h, 0, 0));
   }
-  issue_half<false>(a.k_rsrc, lds.k[0], 0, wave, lane);
-  if (a.nT > 1) issue_half<false>(a.k_rsrc, lds.k[1], kTileKeys, wave, lane);
-  issue_half<true>(a.v_rsrc, lds.v[0], 0, wave, lane);
+  issue_half<false>(a.k_rsrc, a.k_row_bytes, lds.k[0], 0, wave, lane);
+  if (a.nT > 1) issue_half<false>(a.k_rsrc, a.k_row_bytes, lds.k[1], kTileKeys, wave, lane);
+  issue_half<true>(a.v_rsrc, a.v_row_bytes, lds.v[0], 0, wave, lane);
 
   // K A-operand, d chunk c: row r32 (+32 for the second key half, an immediate), logical 16-B
   // chunk 2c + h.
@@ -515,7 +535,8 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
 
   if (qrow < N) {
     const float inv_l = 1.0f / w.l_run;
-    __bf16* orow = O + head_off + (size_t)qrow * kD;
+    __bf16* orow = kDense ? O + dense_head + (long long)qrow * kD
+                          : O + bb * os.b + hh * os.h + (long long)qrow * os.n;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       bf16x4 lo4, hi4;
@@ -547,25 +568,108 @@ constexpr int kMaxDevices = 64;
 static std::once_flag g_dev_once[kMaxDevices];
 static DeviceInfo g_dev_info[kMaxDevices];
 
-// Argument checks, in this order: sizes and flags first, then - only for a non-empty
+// Element strides of one operand as the kernel uses them.  A null `st` is the contiguous
+// (B, H, N, 64) layout.  The stride of a dimension of size 1 is never used (it may hold
+// anything, as in torch), so it is replaced by 0 (b, h) or 64 (n).
+static Strides operand_strides(const int64_t* st, int B, int H, int N) {
+  Strides s;
+  s.b = B == 1 ? 0 : st ? st[0] : (long long)H * N * kD;
+  s.h = H == 1 ? 0 : st ? st[1] : (long long)N * kD;
+  s.n = N == 1 ? kD : st ? st[2] : kD;
+  return s;
+}
+
+// Stride rules (elements): the last dimension is dense (stride 1); the row stride is at least
+// 64, so rows of one head do not overlap and row N starts where a buffer descriptor over N
+// rows ends; every stride is a non-negative multiple of 8, so every row start keeps the
+// 16-byte alignment of the base pointer; the largest per-head buffer offset,
+// (N + 128) rows * row stride * 2 bytes, fits the 32-bit offset of a buffer access.
+static int check_strides(const int64_t* st, int B, int H, int N) {
+  if (st == nullptr) return TFGFA_OK;
+  if (st[3] != 1) return TFGFA_ERR_STRIDE;
+  const Strides s = operand_strides(st, B, H, N);
+  if (s.b < 0 || s.h < 0 || s.n < kD) return TFGFA_ERR_STRIDE;
+  if ((s.b | s.h | s.n) & 7) return TFGFA_ERR_STRIDE;
+  if (s.n > INT32_MAX / 2 || ((long long)N + kBlockRows) * s.n * 2 > INT32_MAX)
+    return TFGFA_ERR_TOO_LARGE;
+  return TFGFA_OK;
+}
+
+// O must not write one element twice: with its dimensions of size > 1 sorted by stride, each
+// stride must exceed the largest offset reachable through the smaller ones (a sufficient
+// condition for distinct offsets; every layout torch makes by viewing a buffer meets it).
+static bool overlaps(const int64_t* st, int B, int H, int N) {
+  if (st == nullptr) return false;
+  const Strides s = operand_strides(st, B, H, N);
+  long long stride[3] = {s.b, s.h, s.n};
+  long long size[3] = {B, H, N};
+  for (int i = 0; i < 3; ++i)  // insertion sort by stride, 3 elements
+    for (int j = i; j > 0 && stride[j] < stride[j - 1]; --j) {
+      const long long ts = stride[j], tz = size[j];
+      stride[j] = stride[j - 1];
+      size[j] = size[j - 1];
+      stride[j - 1] = ts;
+      size[j - 1] = tz;
+    }
+  long long reach = kD - 1;  // the dense last dimension
+  for (int i = 0; i < 3; ++i) {
+    if (size[i] == 1) continue;
+    if (stride[i] <= reach) return true;
+    reach += (size[i] - 1) * stride[i];
+  }
+  return false;
+}
+
+// Argument checks, in this order: sizes, flags and strides first, then - only for a non-empty
 // problem - pointers.  An empty tensor may legitimately have a null data pointer
 // (torch gives numel()==0 tensors address 0), so B, H or N == 0 succeeds with no launch.
 static int validate(const void* q, const void* k, const void* v, const void* o, const float* lse,
-                    int B, int H, int N, int D, float scale, int causal) {
+                    int B, int H, int N, int D, float scale, int causal, const int64_t* const* st) {
   if (B < 0 || H < 0 || N < 0) return TFGFA_ERR_BAD_SHAPE;
   if (D != kD) return TFGFA_ERR_HEAD_DIM;
   if (!(scale > 0.f) || !isfinite(scale)) return TFGFA_ERR_SCALE;
   if (causal != 0 && causal != 1) return TFGFA_ERR_CAUSAL_FLAG;
   if (B == 0 || H == 0 || N == 0) return TFGFA_OK;
-  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr) return TFGFA_ERR_NULL_POINTER;
-  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15u) return TFGFA_ERR_ALIGNMENT;
-  if (((uintptr_t)lse) & 3u) return TFGFA_ERR_ALIGNMENT;
   const long long bh = (long long)B * H;
   const long long nqb = ((long long)N + kBlockRows - 1) / kBlockRows;
   if (bh > INT32_MAX || bh * nqb > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
-  // Per-head byte offsets (row * 128 B) are 32-bit buffer offsets.
+  // Per-head byte offsets (row * 128 B for a contiguous head) are 32-bit buffer offsets.
   if (((long long)N + kBlockRows) * kKRowBytes > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
+  for (int i = 0; i < 4; ++i) {
+    const int sst = check_strides(st[i], B, H, N);
+    if (sst != TFGFA_OK) return sst;
+  }
+  if (overlaps(st[3], B, H, N)) return TFGFA_ERR_STRIDE;
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr) return TFGFA_ERR_NULL_POINTER;
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15u) return TFGFA_ERR_ALIGNMENT;
+  if (((uintptr_t)lse) & 3u) return TFGFA_ERR_ALIGNMENT;
   return TFGFA_OK;
+}
+
+static int launch(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
+                  int N, int D, float softmax_scale, int causal, void* hip_stream,
+                  const int64_t* const* st) {
+  const int vst = validate(q, k, v, o, lse, B, H, N, D, softmax_scale, causal, st);
+  if (vst != TFGFA_OK) return vst;
+  if (B == 0 || H == 0 || N == 0) return TFGFA_OK;
+
+  const int BH = B * H;
+  const int nQB = (N + kBlockRows - 1) / kBlockRows;
+  const float scale_log2 = softmax_scale * kLog2e;
+  const Strides qs = operand_strides(st[0], B, H, N), ks = operand_strides(st[1], B, H, N),
+                vs = operand_strides(st[2], B, H, N), os = operand_strides(st[3], B, H, N);
+  const Strides dense = operand_strides(nullptr, B, H, N);
+  auto same = [](const Strides& x, const Strides& y) {
+    return x.b == y.b && x.h == y.h && x.n == y.n;
+  };
+  const bool all_dense = same(qs, dense) && same(ks, dense) && same(vs, dense) && same(os, dense);
+  hipLaunchKernelGGL(all_dense ? fwd_kernel<true> : fwd_kernel<false>, dim3(BH * nQB),
+                     dim3(kThreads), 0, (hipStream_t)hip_stream, static_cast<const __bf16*>(q),
+                     static_cast<const __bf16*>(k), static_cast<const __bf16*>(v),
+                     static_cast<__bf16*>(o), lse, H, BH, N, nQB, scale_log2, causal, qs, ks, vs,
+                     os);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TFGFA_OK : -(int)e;
 }
 
 }  // namespace tfgfa
@@ -573,20 +677,18 @@ static int validate(const void* q, const void* k, const void* v, const void* o, 
 extern "C" int tfgfa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
                               int B, int H, int N, int D, float softmax_scale, int causal,
                               void* hip_stream) {
-  using namespace tfgfa;
-  const int st = validate(q, k, v, o, lse, B, H, N, D, softmax_scale, causal);
-  if (st != TFGFA_OK) return st;
-  if (B == 0 || H == 0 || N == 0) return TFGFA_OK;
+  const int64_t* const contiguous[4] = {nullptr, nullptr, nullptr, nullptr};
+  return tfgfa::launch(q, k, v, o, lse, B, H, N, D, softmax_scale, causal, hip_stream,
+                       contiguous);
+}
 
-  const int BH = B * H;
-  const int nQB = (N + kBlockRows - 1) / kBlockRows;
-  const float scale_log2 = softmax_scale * kLog2e;
-  hipLaunchKernelGGL(fwd_kernel, dim3(BH * nQB), dim3(kThreads), 0, (hipStream_t)hip_stream,
-                     static_cast<const __bf16*>(q), static_cast<const __bf16*>(k),
-                     static_cast<const __bf16*>(v), static_cast<__bf16*>(o), lse, BH, N, nQB,
-                     scale_log2, causal);
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? TFGFA_OK : -(int)e;
+extern "C" int tfgfa_fwd_bf16_strided(const void* q, const int64_t* q_strides, const void* k,
+                                      const int64_t* k_strides, const void* v,
+                                      const int64_t* v_strides, void* o,
+                                      const int64_t* o_strides, float* lse, int B, int H, int N,
+                                      int D, float softmax_scale, int causal, void* hip_stream) {
+  const int64_t* const st[4] = {q_strides, k_strides, v_strides, o_strides};
+  return tfgfa::launch(q, k, v, o, lse, B, H, N, D, softmax_scale, causal, hip_stream, st);
 }
 
 extern "C" const char* tfgfa_strerror(int status) {
@@ -599,6 +701,9 @@ extern "C" const char* tfgfa_strerror(int status) {
     case TFGFA_ERR_CAUSAL_FLAG: return "causal flag must be 0 or 1";
     case TFGFA_ERR_TOO_LARGE: return "problem exceeds the launch limits (B*H*ceil(N/128) < 2^31)";
     case TFGFA_ERR_ALIGNMENT: return "misaligned pointer (q/k/v/o need 16 B, lse 4 B)";
+    case TFGFA_ERR_STRIDE:
+      return "unsupported strides (last dim 1; b, h, n non-negative multiples of 8; n >= 64; "
+             "o without overlapping elements)";
     default: break;
   }
   if (status < 0) return hipGetErrorString((hipError_t)(-status));

@@ -7,7 +7,9 @@
 // C-ABI status becomes a Python RuntimeError (the reference drops launcher errors,
 // torch_bind.cpp:34-39).
 #include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
 
+#include <array>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -34,6 +36,27 @@ void fwd(std::uintptr_t q, std::uintptr_t k, std::uintptr_t v, std::uintptr_t o,
   }
 }
 
+using Strides4 = std::array<std::int64_t, 4>;
+
+void fwd_strided(std::uintptr_t q, const Strides4& qs, std::uintptr_t k, const Strides4& ks,
+                 std::uintptr_t v, const Strides4& vs, std::uintptr_t o, const Strides4& os,
+                 std::uintptr_t lse, int B, int H, int N, int D, float softmax_scale, bool causal,
+                 std::uintptr_t stream) {
+  int st;
+  {
+    py::gil_scoped_release nogil;
+    st = tfgfa_fwd_bf16_strided(
+        reinterpret_cast<const void*>(q), qs.data(), reinterpret_cast<const void*>(k), ks.data(),
+        reinterpret_cast<const void*>(v), vs.data(), reinterpret_cast<void*>(o), os.data(),
+        reinterpret_cast<float*>(lse), B, H, N, D, softmax_scale, causal ? 1 : 0,
+        reinterpret_cast<void*>(stream));
+  }
+  if (st != TFGFA_OK) {
+    throw std::runtime_error(std::string("tfgfa_fwd_bf16_strided failed (status ") +
+                             std::to_string(st) + "): " + tfgfa_strerror(st));
+  }
+}
+
 py::dict device_info() {
   int cu = 0, mhz = 0;
   char arch[128] = {0};
@@ -55,6 +78,12 @@ PYBIND11_MODULE(_C, m) {
   m.def("fwd", &fwd, "Launch the bf16 attention forward on raw device pointers", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("o"), py::arg("lse"), py::arg("B"), py::arg("H"),
         py::arg("N"), py::arg("D"), py::arg("softmax_scale"), py::arg("causal"),
+        py::arg("stream"));
+  m.def("fwd_strided", &fwd_strided,
+        "Launch the bf16 attention forward on strided operands (element strides b, h, n, d)",
+        py::arg("q"), py::arg("q_strides"), py::arg("k"), py::arg("k_strides"), py::arg("v"),
+        py::arg("v_strides"), py::arg("o"), py::arg("o_strides"), py::arg("lse"), py::arg("B"),
+        py::arg("H"), py::arg("N"), py::arg("D"), py::arg("softmax_scale"), py::arg("causal"),
         py::arg("stream"));
   m.def("device_info", &device_info, "CU count, shader clock (MHz) and arch of the current device");
   m.def("strerror", [](int st) { return std::string(tfgfa_strerror(st)); });

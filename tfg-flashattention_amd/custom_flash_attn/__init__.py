@@ -30,7 +30,7 @@ except ImportError as exc:  # pragma: no cover - exercised only on a broken buil
         f"({exc}); run `make -C tfg-flashattention_amd/csrc` or __graft_entry__.build()"
     ) from exc
 
-__all__ = ["forward", "forward_lse", "device_info", "HEAD_DIM", "library_path"]
+__all__ = ["forward", "forward_lse", "attention", "device_info", "HEAD_DIM", "library_path"]
 
 HEAD_DIM = 64  # the only compiled head dimension (common_types.hpp:33 fixes K = 64 too)
 
@@ -111,6 +111,59 @@ def forward_lse(Q: torch.Tensor, K_mat: torch.Tensor, V: torch.Tensor, /,
     lse = torch.empty(Q.shape[:3], dtype=torch.float32, device=Q.device)
     _launch(Q, K_mat, V, O, lse, scale, causal)
     return O, lse
+
+
+def _check_view(x, name: str, ref) -> None:
+    if not x.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if x.dtype != torch.bfloat16:
+        raise RuntimeError("Unsupported tensor dtype. Use bfloat16.")
+    if x.dim() != 4:
+        raise RuntimeError(f"{name} must be 4-D (batch, heads, seq_len, head_dim), got shape {tuple(x.shape)}")
+    if ref is not None:
+        if x.shape != ref.shape:
+            raise RuntimeError(f"{name} must have shape {tuple(ref.shape)}, got {tuple(x.shape)}")
+        if x.device != ref.device:
+            raise RuntimeError(f"{name} must be on {ref.device}, got {x.device}")
+    if x.shape[3] != HEAD_DIM:
+        raise RuntimeError(f"head_dim must be {HEAD_DIM}, got {x.shape[3]}")
+    if x.stride(3) != 1 and x.shape[3] > 1:
+        raise RuntimeError(f"{name} must be dense in its last dimension (stride 1), got strides {x.stride()}")
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, out: torch.Tensor | None = None,
+              softmax_scale: float | None = None, causal: bool = True, return_lse: bool = False):
+    """Attention forward over strided (B, H, N, 64) bf16 views, with no copies.
+
+    ``q``, ``k``, ``v`` may be any views whose last dimension is dense, e.g. the
+    ``x.view(B, N, H, 64).transpose(1, 2)`` projections of a GPT-2 block
+    (src/py/model_inference.py:64-66), which the reference's caller copies with
+    ``.contiguous()`` first (:86-90).  ``out``, if given, is a (B, H, N, 64) bf16 view
+    the result is written into - pass ``buf.transpose(1, 2)`` of a (B, N, H, 64) buffer
+    and the (B, N, H*64) context needs no transposing copy (:92).  Batch, head and row
+    strides must be non-negative multiples of 8 elements with row stride >= 64 and data
+    16-byte aligned; other layouts raise RuntimeError from the C ABI.  Returns ``out``
+    (a new contiguous tensor when none is given), or ``(out, lse)`` with
+    ``return_lse=True`` (lse contiguous (B, H, N) float32, natural log).
+    """
+    _check_view(q, "q", None)
+    _check_view(k, "k", q)
+    _check_view(v, "v", q)
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    else:
+        _check_view(out, "out", q)
+    B, H, N, D = q.shape
+    scale = (1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
+    lse = torch.empty((B, H, N), dtype=torch.float32, device=q.device) if return_lse else None
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _C.fwd_strided(
+            q.data_ptr(), q.stride(), k.data_ptr(), k.stride(), v.data_ptr(), v.stride(),
+            out.data_ptr(), out.stride(), 0 if lse is None else lse.data_ptr(),
+            B, H, N, D, scale, bool(causal), stream,
+        )
+    return (out, lse) if return_lse else out
 
 
 def device_info() -> dict:

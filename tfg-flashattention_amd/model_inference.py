@@ -9,9 +9,12 @@ download (model_inference.py:23-37, :193-376; gpt_download.py) are not.
 ``impl_type`` selects the attention implementation as at model_inference.py:68-90:
   * ``"manual"``     - the reference's explicit PyTorch path (:68-75);
   * ``"functional"`` - torch.nn.functional.scaled_dot_product_attention (:77-80);
-  * ``"hip"`` (``"cuda"`` accepted as the reference's spelling) - custom_flash_attn.forward,
-    the hand-written gfx950 kernel (:85-90).  There is no fallback: if the extension is
-    missing this raises.
+  * ``"cuda"`` - custom_flash_attn.forward on ``.contiguous()`` copies of Q, K, V, as the
+    reference's branch calls it (:85-90);
+  * ``"hip"`` - the same gfx950 kernel through custom_flash_attn.attention, which reads the
+    (B, H, N, d) views of the projections in place and writes O straight into a (B, N, H, d)
+    buffer: no copies on either side of the kernel.
+  There is no fallback for either: if the extension is missing they raise.
   * ``"triton"`` is not provided (the Triton variant is not rebuilt).
 
 Behaviour difference, on purpose: the reference's "cuda" branch reshapes the kernel's
@@ -49,7 +52,7 @@ def _attn_functional(q, k, v, mask_bool, dropout):
     return F.scaled_dot_product_attention(q, k, v, is_causal=True, dropout_p=p).transpose(1, 2)
 
 
-def _attn_hip(q, k, v, mask_bool, dropout):
+def _attn_cuda(q, k, v, mask_bool, dropout):
     # model_inference.py:85-90, plus the transpose back to (B, N, H, d).
     import custom_flash_attn  # raises if the native extension is not built
 
@@ -57,11 +60,22 @@ def _attn_hip(q, k, v, mask_bool, dropout):
     return out.transpose(1, 2)
 
 
+def _attn_hip(q, k, v, mask_bool, dropout):
+    # Same function as _attn_cuda with the copies fused away: q, k, v are read through their
+    # strides and O lands in (B, N, H, d) order, ready for the .view(b, N, d_out) below.
+    import custom_flash_attn  # raises if the native extension is not built
+
+    b, h, n, d = q.shape
+    out = torch.empty(b, n, h, d, dtype=q.dtype, device=q.device)
+    custom_flash_attn.attention(q, k, v, out=out.transpose(1, 2))
+    return out
+
+
 ATTENTION_IMPLS: Dict[str, Callable] = {
     "manual": _attn_manual,
     "functional": _attn_functional,
     "hip": _attn_hip,
-    "cuda": _attn_hip,
+    "cuda": _attn_cuda,
 }
 
 
