@@ -33,13 +33,14 @@
 #ifndef TFGFA_H
 #define TFGFA_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-#define TFGFA_ABI_VERSION 2
+#define TFGFA_ABI_VERSION 3
 
 /* Status codes (> 0: invalid argument). */
 #define TFGFA_OK                 0
@@ -50,7 +51,8 @@ extern "C" {
 #define TFGFA_ERR_CAUSAL_FLAG    5  /* causal is neither 0 nor 1                     */
 #define TFGFA_ERR_TOO_LARGE      6  /* grid or element count exceeds the limits      */
 #define TFGFA_ERR_ALIGNMENT      7  /* q/k/v/o not 16-byte aligned or lse not 4-byte */
-#define TFGFA_ERR_STRIDE         8  /* strides outside what tfgfa_fwd_bf16_strided takes */
+#define TFGFA_ERR_STRIDE         8  /* strides outside what the entry point takes         */
+#define TFGFA_ERR_CACHE          9  /* k_new/v_new given without cache_seqlens            */
 
 /*
  * Attention forward, bf16 in / bf16 out, fp32 accumulation and softmax.
@@ -96,6 +98,57 @@ int tfgfa_fwd_bf16_strided(const void* q, const int64_t* q_strides,
                            void* o, const int64_t* o_strides, float* lse,
                            int B, int H, int N, int D, float softmax_scale, int causal,
                            void* hip_stream);
+
+/*
+ * One decode step over a KV cache: attention of one new query per (batch, head)
+ * over the cached keys, bf16 in / bf16 out, fp32 softmax.
+ *
+ *   L_b = cache_seqlens[b] (+1 when appending), or N_max when cache_seqlens is NULL
+ *   O[b,h,:]  = sum_{j < L_b} softmax_j(scale * q[b,h,:] . K[b,h,j,:]) * V[b,h,j,:]
+ *   LSE[b,h]  = log sum_{j < L_b} exp(scale * q[b,h,:] . K[b,h,j,:])
+ *
+ * That is the last row of the causal forward over the first L_b tokens.  The
+ * reference has no such step: its generate() re-runs the whole prefix through
+ * the model for every new token (src/py/model_inference.py:199-228, timed at
+ * :444-457), computing this row as part of a full causal forward.
+ *
+ * Operands (element strides, last dimension dense, other strides non-negative
+ * multiples of 8, as Tensor.stride() gives them):
+ *   q, o              (B, H, 64)        strides [b, h, d]
+ *   k_cache, v_cache  (B, H, N_max, 64) strides [b, h, n, d], n >= 64
+ *   k_new, v_new      (B, H, 64)        strides [b, h, d]; both NULL or both set
+ *   cache_seqlens     B int32 in device memory, valid cached rows per batch row
+ *   lse               (B, H) float32 contiguous, or NULL
+ * With k_new/v_new set (requires cache_seqlens, else TFGFA_ERR_CACHE), row
+ * L = cache_seqlens[b] of each cache receives k_new/v_new and attention covers
+ * L + 1 keys; the caller advances cache_seqlens afterwards.  L_b = 0 gives
+ * O = 0 and LSE = -inf.  A length that does not fit (cache_seqlens[b] < 0 or
+ * cache_seqlens[b] + append > N_max) is only visible on the device: that batch
+ * row gets NaN in O and LSE, and nothing is appended or read for it.
+ *
+ * workspace: device memory for split-sequence partials (16-byte aligned), or
+ * NULL.  The cache sequence is split over up to
+ * tfgfa_decode_workspace_bytes(B, H, N_max) / (B*H*260) workgroups per head,
+ * merged by a second kernel; with NULL (or too small for two splits) each head
+ * is one workgroup, correct but slower for small B*H.  Calls sharing a
+ * workspace must be ordered on one stream.
+ */
+int tfgfa_decode_bf16(const void* q, const int64_t* q_strides,
+                      void* k_cache, const int64_t* k_strides,
+                      void* v_cache, const int64_t* v_strides,
+                      const void* k_new, const int64_t* k_new_strides,
+                      const void* v_new, const int64_t* v_new_strides,
+                      const int* cache_seqlens,
+                      void* o, const int64_t* o_strides, float* lse,
+                      int B, int H, int N_max, int D, float softmax_scale,
+                      void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/*
+ * Workspace bytes that let tfgfa_decode_bf16 use every split it may choose
+ * for these sizes (0 when B, H or N_max is not positive).  Independent of the
+ * device.  No counterpart in the reference.
+ */
+size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max);
 
 /*
  * Human-readable text for a status code returned by any tfgfa_* function.

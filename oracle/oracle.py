@@ -129,6 +129,38 @@ def attention_c(q, k, v, scale: float | None = None, causal: bool = True, rows=N
     return o, lse
 
 
+def decode_np(q, k_cache, v_cache, lens, scale: float | None = None):
+    """One decode step over a KV cache, fp64: the last row of the causal forward.
+
+    The reference has no KV cache; its generate() recomputes the causal forward over the
+    prefix for every new token (src/py/model_inference.py:199-228) and keeps the last row,
+    whose value under the "manual" branch (:68-75) is
+        o = softmax_j(scale * q . k_j) v_j over j < L,   lse = log sum_j exp(scale * q . k_j).
+    q: (B, H, D); k_cache, v_cache: (B, H, N_max, D); lens: B ints (keys attended per batch
+    row, 0 <= L <= N_max).  Returns (o (B, H, D), lse (B, H)) in float64; L = 0 gives o = 0,
+    lse = -inf.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k_cache = np.asarray(k_cache, dtype=np.float64)
+    v_cache = np.asarray(v_cache, dtype=np.float64)
+    B, H, D = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    o = np.zeros((B, H, D), dtype=np.float64)
+    lse = np.full((B, H), -np.inf, dtype=np.float64)
+    for b in range(B):
+        L = int(lens[b])
+        if L == 0:
+            continue
+        s = np.einsum("hjd,hd->hj", k_cache[b, :, :L], q[b]) * scale
+        m = s.max(axis=-1, keepdims=True)
+        p = np.exp(s - m)
+        l = p.sum(axis=-1, keepdims=True)
+        o[b] = np.einsum("hj,hjd->hd", p / l, v_cache[b, :, :L])
+        lse[b] = (m + np.log(l))[:, 0]
+    return o, lse
+
+
 def manual_attention_torch(q, k, v):
     """The reference's PyTorch CPU attention path, fp32 (src/py/model_inference.py:68-75).
 

@@ -36,6 +36,12 @@ def lib():
     lib.tfgfa_fwd_bf16_strided.restype = ctypes.c_int
     lib.tfgfa_fwd_bf16_strided.argtypes = [ctypes.c_void_p, ctypes.c_void_p] * 4 + [ctypes.c_void_p] + [
         ctypes.c_int] * 4 + [ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
+    lib.tfgfa_decode_bf16.restype = ctypes.c_int
+    lib.tfgfa_decode_bf16.argtypes = [ctypes.c_void_p, ctypes.c_void_p] * 5 + [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 4 + [
+        ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.tfgfa_decode_workspace_bytes.restype = ctypes.c_size_t
+    lib.tfgfa_decode_workspace_bytes.argtypes = [ctypes.c_int] * 3
     lib.tfgfa_strerror.restype = ctypes.c_char_p
     lib.tfgfa_strerror.argtypes = [ctypes.c_int]
     lib.tfgfa_abi_version.restype = ctypes.c_int
@@ -44,8 +50,9 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     names = _header_functions()
-    assert names == ["tfgfa_abi_version", "tfgfa_device_info", "tfgfa_fwd_bf16",
-                     "tfgfa_fwd_bf16_strided", "tfgfa_strerror"]
+    assert names == ["tfgfa_abi_version", "tfgfa_decode_bf16", "tfgfa_decode_workspace_bytes",
+                     "tfgfa_device_info", "tfgfa_fwd_bf16", "tfgfa_fwd_bf16_strided",
+                     "tfgfa_strerror"]
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/tfgfa.h but not exported"
 
@@ -59,7 +66,7 @@ def test_strerror_covers_every_status(lib):
     codes = [_header_define(n) for n in (
         "TFGFA_OK", "TFGFA_ERR_NULL_POINTER", "TFGFA_ERR_BAD_SHAPE", "TFGFA_ERR_HEAD_DIM",
         "TFGFA_ERR_SCALE", "TFGFA_ERR_CAUSAL_FLAG", "TFGFA_ERR_TOO_LARGE", "TFGFA_ERR_ALIGNMENT",
-        "TFGFA_ERR_STRIDE")]
+        "TFGFA_ERR_STRIDE", "TFGFA_ERR_CACHE")]
     msgs = [lib.tfgfa_strerror(c).decode() for c in codes]
     assert len(set(msgs)) == len(msgs)
     assert lib.tfgfa_strerror(12345).decode() == "unknown tfgfa status"
@@ -170,6 +177,75 @@ def test_pybind_strided_raises_runtime_error_with_message():
         _C.fwd_strided(P, (64 * 16, 64 * 16, 32, 1), P, c, P, c, P, c, 0, 1, 1, 16, 64, 0.125, True, 0)
     with pytest.raises(RuntimeError, match="tfgfa_fwd_bf16_strided failed"):
         _C.fwd_strided(0, c, P, c, P, c, P, c, 0, 1, 1, 16, 64, 0.125, True, 0)
+
+
+# Decode entry point.  q, o, k_new, v_new: (B, H, 64) with strides [b, h, d]; caches
+# (B, H, N_max, 64) with [b, h, n, d].  Every case stops before any HIP call.
+def _s3(*v):
+    return (ctypes.c_int64 * 3)(*v)
+
+
+def _decode_args(B=2, H=3, N=100, q=None, kc=None, vc=None, kn=None, vn=None, seq=None, o=None,
+                 lse=None, qs=None, ks=None, vs=None, kns=None, vns=None, os_=None, D=64,
+                 scale=0.125, ws=None, ws_bytes=0):
+    qs = qs or _s3(H * 64, 64, 1)
+    ks = ks or _st(H * N * 64, N * 64, 64, 1)
+    vs = vs or _st(H * N * 64, N * 64, 64, 1)
+    kns = kns or _s3(H * 64, 64, 1)
+    vns = vns or _s3(H * 64, 64, 1)
+    os_ = os_ or _s3(H * 64, 64, 1)
+    return (q, qs, kc, ks, vc, vs, kn, kns, vn, vns, seq, o, os_, lse, B, H, N, D, scale, ws,
+            ws_bytes, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=-1), "TFGFA_ERR_BAD_SHAPE"),
+    (dict(N=-5), "TFGFA_ERR_BAD_SHAPE"),
+    (dict(D=128), "TFGFA_ERR_HEAD_DIM"),
+    (dict(scale=0.0), "TFGFA_ERR_SCALE"),
+    (dict(scale=float("nan")), "TFGFA_ERR_SCALE"),
+    (dict(kn=P), "TFGFA_ERR_NULL_POINTER"),                     # k_new without v_new
+    (dict(kn=P, vn=P), "TFGFA_ERR_CACHE"),                      # append needs cache_seqlens
+    (dict(B=0), "TFGFA_OK"),                                    # empty: nothing launched
+    (dict(H=0, kn=P, vn=P, seq=P), "TFGFA_OK"),
+    (dict(), "TFGFA_ERR_NULL_POINTER"),                         # strides accepted, q NULL
+    (dict(qs=_s3(192, 64, 2)), "TFGFA_ERR_STRIDE"),             # q dim not dense
+    (dict(qs=_s3(192, 60, 1)), "TFGFA_ERR_STRIDE"),             # q head stride not a multiple of 8
+    (dict(ks=_st(3 * 100 * 64, 100 * 64, 32, 1)), "TFGFA_ERR_STRIDE"),   # overlapping cache rows
+    (dict(vs=_st(3 * 100 * 72, 100 * 72, 68, 1)), "TFGFA_ERR_STRIDE"),   # 136-byte rows
+    (dict(ks=_st(3 * 100 * 64, 100 * 64, 64, 2)), "TFGFA_ERR_STRIDE"),
+    (dict(os_=_s3(64, 64, 1)), "TFGFA_ERR_STRIDE"),             # O rows of two batches collide
+    (dict(os_=_s3(0, 64, 1)), "TFGFA_ERR_STRIDE"),
+    (dict(kn=P, vn=P, seq=P, kns=_s3(192, 64, 3)), "TFGFA_ERR_STRIDE"),
+    (dict(q=P, kc=P, vc=P, o=P, B=1, H=1, qs=_s3(7, 5, 1), os_=_s3(3, 9, 1), ks=_st(1, 2, 64, 1),
+          vs=_st(1, 2, 64, 1), lse=P + 2), "TFGFA_ERR_ALIGNMENT"),  # size-1 strides ignored
+    (dict(N=1 << 24), "TFGFA_ERR_TOO_LARGE"),
+    (dict(q=P + 8, kc=P, vc=P, o=P), "TFGFA_ERR_ALIGNMENT"),
+    (dict(q=P, kc=P, vc=P, o=P, seq=P + 2), "TFGFA_ERR_ALIGNMENT"),
+    (dict(q=P, kc=P, vc=P, o=P, ws=P + 8, ws_bytes=4096), "TFGFA_ERR_ALIGNMENT"),
+    (dict(q=P, kc=None, vc=P, o=P), "TFGFA_ERR_NULL_POINTER"),
+])
+def test_c_abi_decode_validation(lib, kw, code):
+    assert lib.tfgfa_decode_bf16(*_decode_args(**kw)) == _header_define(code)
+
+
+def test_decode_workspace_bytes(lib):
+    assert lib.tfgfa_decode_workspace_bytes(8, 25, 1024) == 8 * 25 * 8 * 65 * 4
+    assert lib.tfgfa_decode_workspace_bytes(1, 1, 1) == 65 * 4
+    assert lib.tfgfa_decode_workspace_bytes(1, 16, 8193) == 16 * 65 * 65 * 4
+    for bad in ((0, 1, 1), (1, 0, 1), (1, 1, 0), (-1, 2, 3)):
+        assert lib.tfgfa_decode_workspace_bytes(*bad) == 0
+    assert _C.decode_workspace_bytes(8, 25, 1024) == lib.tfgfa_decode_workspace_bytes(8, 25, 1024)
+
+
+def test_pybind_decode_raises_runtime_error_with_message():
+    z3 = (0, 0, 0)
+    with pytest.raises(RuntimeError, match="tfgfa_decode_bf16 failed .*cache_seqlens"):
+        _C.decode(P, (192, 64, 1), P, (19200, 6400, 64, 1), P, (19200, 6400, 64, 1), P, (192, 64, 1),
+                  P, (192, 64, 1), 0, P, (192, 64, 1), 0, 2, 3, 100, 64, 0.125, 0, 0, 0)
+    with pytest.raises(RuntimeError, match="unsupported head dimension"):
+        _C.decode(P, z3, P, (0, 0, 0, 1), P, (0, 0, 0, 1), 0, z3, 0, z3, 0, P, z3, 0,
+                  2, 3, 100, 32, 0.125, 0, 0, 0)
 
 
 def test_pybind_raises_runtime_error_with_message():

@@ -1,0 +1,231 @@
+"""Decode step over a KV cache (tfgfa_decode_bf16) against the CPU oracle (GPU box only).
+
+The oracle is ``decode_np``: the last row of the causal forward over the first L cached
+tokens (what the reference's generate() recomputes per token, src/py/model_inference.py:
+199-228), pinned in tests/test_oracle.py.  Tolerances as for the forward: max|dO| <= 2e-2,
+mean|dO| <= 2e-3, max|dLSE| <= 1e-3, on Q, K ~ N(0, 3^2) (wide logits) and V ~ N(0, 1).
+
+Covered: ragged lengths (1 .. N_max), the fused append of the new token (cache row written,
+nothing else touched), the split-sequence path against the one-workgroup path, strided
+caches and views (bitwise equal to contiguous ones), long caches, L = 0, invalid lengths
+(NaN for that row only, nothing appended), agreement with the forward kernel's last row.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16_round, decode_np
+
+import custom_flash_attn
+from custom_flash_attn import _C
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TOL_MAX, TOL_MEAN, TOL_LSE = 2e-2, 2e-3, 1e-3
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _rand(shape, seed, sigma=1.0):
+    g = np.random.Generator(np.random.PCG64(seed))
+    return bf16_round(g.standard_normal(shape, dtype=np.float32) * np.float32(sigma))
+
+
+def _dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(torch.bfloat16).to(DEV)
+
+
+def _check(o, lse, o_ref, lse_ref, label, rows=None):
+    o = o.float().cpu().numpy().astype(np.float64)
+    lse = lse.cpu().numpy().astype(np.float64)
+    if rows is not None:
+        o, lse, o_ref, lse_ref = o[rows], lse[rows], o_ref[rows], lse_ref[rows]
+    d = np.abs(o - o_ref)
+    fin = np.isfinite(lse_ref)
+    dl = np.abs(lse[fin] - lse_ref[fin])
+    _say(f"{label}: max|dO|={d.max():.3e} mean|dO|={d.mean():.3e} "
+         f"max|dLSE|={dl.max() if dl.size else 0:.3e}")
+    assert np.isfinite(o).all(), f"{label}: non-finite O"
+    assert np.array_equal(np.isneginf(lse), ~fin), f"{label}: -inf LSE pattern differs"
+    assert d.max() <= TOL_MAX and d.mean() <= TOL_MEAN, label
+    assert dl.size == 0 or dl.max() <= TOL_LSE, label
+
+
+def _case(B, H, N_max, seed):
+    kc = _rand((B, H, N_max, 64), seed, 3.0)
+    vc = _rand((B, H, N_max, 64), seed + 1)
+    q = _rand((B, H, 64), seed + 2, 3.0)
+    return q, kc, vc
+
+
+@pytest.mark.parametrize("B,H,N_max,lens", [
+    (3, 5, 700, [1, 345, 700]),
+    (2, 4, 128, [128, 127]),
+    (4, 2, 257, [129, 256, 2, 257]),
+    (1, 16, 8192, [8192]),
+    (2, 3, 5000, [4097, 3]),
+])
+def test_decode_matches_oracle(B, H, N_max, lens):
+    _say(f"decode B={B} H={H} N_max={N_max} lens={lens}")
+    q, kc, vc = _case(B, H, N_max, 1000 + N_max)
+    o_ref, l_ref = decode_np(q, kc, vc, lens, 0.125)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    o, lse = custom_flash_attn.decode(_dev(q), _dev(kc), _dev(vc), sl, return_lse=True)
+    torch.cuda.synchronize()
+    _check(o, lse, o_ref, l_ref, f"decode N_max={N_max}")
+
+
+def test_decode_all_rows_when_no_lengths():
+    B, H, N_max = 2, 3, 333
+    q, kc, vc = _case(B, H, N_max, 77)
+    o_ref, l_ref = decode_np(q, kc, vc, [N_max] * B, 0.3)
+    o, lse = custom_flash_attn.decode(_dev(q), _dev(kc), _dev(vc), softmax_scale=0.3, return_lse=True)
+    torch.cuda.synchronize()
+    _check(o, lse, o_ref, l_ref, "no cache_seqlens")
+
+
+@pytest.mark.parametrize("lens", [[0, 100, 699], [5, 383, 384]])
+def test_decode_append_writes_row_and_attends_it(lens):
+    B, H, N_max = 3, 4, 700
+    _say(f"append lens={lens}")
+    q, kc, vc = _case(B, H, N_max, 91)
+    kn, vn = _rand((B, H, 64), 95, 3.0), _rand((B, H, 64), 96)
+    kcd, vcd = _dev(kc), _dev(vc)
+    k_before, v_before = kcd.clone(), vcd.clone()
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    o, lse = custom_flash_attn.decode(_dev(q), kcd, vcd, sl, _dev(kn), _dev(vn), return_lse=True)
+    torch.cuda.synchronize()
+    k_exp, v_exp = k_before.clone(), v_before.clone()
+    for b, L in enumerate(lens):
+        k_exp[b, :, L] = _dev(kn)[b]
+        v_exp[b, :, L] = _dev(vn)[b]
+    assert torch.equal(kcd.view(torch.int16), k_exp.view(torch.int16)), "k_cache: wrong rows written"
+    assert torch.equal(vcd.view(torch.int16), v_exp.view(torch.int16)), "v_cache: wrong rows written"
+    assert torch.equal(sl.cpu(), torch.tensor(lens, dtype=torch.int32)), "cache_seqlens modified"
+    kc2, vc2 = kc.copy(), vc.copy()
+    for b, L in enumerate(lens):
+        kc2[b, :, L], vc2[b, :, L] = kn[b], vn[b]
+    o_ref, l_ref = decode_np(q, kc2, vc2, [L + 1 for L in lens], 0.125)
+    _check(o, lse, o_ref, l_ref, f"append lens={lens}")
+
+
+def test_split_and_single_workgroup_paths_agree():
+    """No workspace forces one workgroup per head; both paths against the oracle."""
+    B, H, N_max = 2, 2, 3000
+    q, kc, vc = _case(B, H, N_max, 123)
+    lens = [2999, 1500]
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    o_ref, l_ref = decode_np(q, kc, vc, lens, 0.125)
+    empty = torch.empty(0, dtype=torch.uint8, device=DEV)
+    o1, l1 = custom_flash_attn.decode(_dev(q), _dev(kc), _dev(vc), sl, return_lse=True, workspace=empty)
+    o2, l2 = custom_flash_attn.decode(_dev(q), _dev(kc), _dev(vc), sl, return_lse=True)
+    torch.cuda.synchronize()
+    _check(o1, l1, o_ref, l_ref, "single workgroup")
+    _check(o2, l2, o_ref, l_ref, "split")
+    assert _C.decode_workspace_bytes(B, H, N_max) == B * H * ((N_max + 127) // 128) * 65 * 4
+
+
+def test_strided_cache_and_views_are_bitwise_equal():
+    """(B, N_max, H, 64) caches, q from a (B, 1, H*64) projection, O into a (B, H*64) row."""
+    B, H, N_max = 3, 5, 600
+    q, kc, vc = _case(B, H, N_max, 55)
+    lens = [600, 17, 300]
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    o_ref, l_ref = custom_flash_attn.decode(_dev(q), _dev(kc), _dev(vc), sl, return_lse=True)
+    kcs = _dev(kc).transpose(1, 2).contiguous().transpose(1, 2)   # (B, N, H, 64) storage
+    vcs = _dev(vc).transpose(1, 2).contiguous().transpose(1, 2)
+    qbuf = torch.zeros(B, 1, 3 * H * 64, dtype=torch.bfloat16, device=DEV)
+    qbuf[:, 0, H * 64:2 * H * 64] = _dev(q).reshape(B, H * 64)
+    qv = qbuf[:, 0, H * 64:2 * H * 64].view(B, H, 64)
+    obuf = torch.full((B, H * 64 + 8), 7.0, dtype=torch.bfloat16, device=DEV)
+    ov = obuf[:, :H * 64].view(B, H, 64)
+    o, lse = custom_flash_attn.decode(qv, kcs, vcs, sl, out=ov, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16))
+    assert torch.equal(lse, l_ref)
+    assert (obuf[:, H * 64:] == 7.0).all(), "padding after O written"
+
+
+def test_matches_forward_kernel_last_row():
+    """Decode with append of token N-1 vs the causal forward kernel's row N-1."""
+    B, H, N = 2, 3, 777
+    q4, k4, v4 = _rand((B, H, N, 64), 61, 3.0), _rand((B, H, N, 64), 62, 3.0), _rand((B, H, N, 64), 63)
+    of, lf = custom_flash_attn.forward_lse(_dev(q4), _dev(k4), _dev(v4))
+    kc = np.zeros((B, H, N, 64), np.float32)
+    vc = np.zeros((B, H, N, 64), np.float32)
+    kc[:, :, :N - 1], vc[:, :, :N - 1] = k4[:, :, :N - 1], v4[:, :, :N - 1]
+    sl = torch.full((B,), N - 1, dtype=torch.int32, device=DEV)
+    kcd, vcd = _dev(kc), _dev(vc)
+    od, ld = custom_flash_attn.decode(_dev(q4[:, :, N - 1]), kcd, vcd, sl, _dev(k4[:, :, N - 1]),
+                                      _dev(v4[:, :, N - 1]), return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(kcd, _dev(k4)) and torch.equal(vcd, _dev(v4))
+    d = (od.float() - of[:, :, N - 1].float()).abs()
+    dl = (ld - lf[:, :, N - 1]).abs()
+    _say(f"decode vs forward row N-1: max|dO|={d.max().item():.3e} max|dLSE|={dl.max().item():.3e}")
+    assert d.max().item() <= 2e-2 and dl.max().item() <= 1e-3
+
+
+def test_invalid_lengths_give_nan_rows_only():
+    B, H, N_max = 4, 2, 300
+    q, kc, vc = _case(B, H, N_max, 200)
+    kn, vn = _rand((B, H, 64), 201, 3.0), _rand((B, H, 64), 202)
+    lens = [-1, 300, 10, 0]    # -1 and 300 (+1 appended > N_max) are invalid
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    kcd, vcd = _dev(kc), _dev(vc)
+    k0, v0 = kcd.clone(), vcd.clone()
+    o, lse = custom_flash_attn.decode(_dev(q), kcd, vcd, sl, _dev(kn), _dev(vn), return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isnan(o[:2].float()).all() and torch.isnan(lse[:2]).all()
+    assert torch.equal(kcd[:2], k0[:2]) and torch.equal(vcd[:2], v0[:2]), "invalid rows appended"
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[2, :, 10], vc2[2, :, 10] = kn[2], vn[2]
+    kc2[3, :, 0], vc2[3, :, 0] = kn[3], vn[3]
+    o_ref, l_ref = decode_np(q, kc2, vc2, [0, 0, 11, 1], 0.125)
+    _check(o, lse, o_ref, l_ref, "valid rows next to invalid ones", rows=[2, 3])
+
+
+def test_zero_length_gives_zero_and_neg_inf():
+    B, H, N_max = 2, 2, 64
+    q, kc, vc = _case(B, H, N_max, 210)
+    sl = torch.tensor([0, 64], dtype=torch.int32, device=DEV)
+    o, lse = custom_flash_attn.decode(_dev(q), _dev(kc), _dev(vc), sl, return_lse=True)
+    torch.cuda.synchronize()
+    assert (o[0] == 0).all() and torch.isneginf(lse[0]).all()
+    o_ref, l_ref = decode_np(q, kc, vc, [0, 64], 0.125)
+    _check(o, lse, o_ref, l_ref, "L=0 next to L=64", rows=[1])
+
+
+def test_gpt2_xl_decode_shape_sampled_heads():
+    """The bench shape: B=8, H=25, 1024-row cache, append of token 1023."""
+    B, H, N_max = 8, 25, 1024
+    q, kc, vc = _case(B, H, N_max, 300)
+    kn, vn = _rand((B, H, 64), 301, 3.0), _rand((B, H, 64), 302)
+    sl = torch.full((B,), N_max - 1, dtype=torch.int32, device=DEV)
+    o, lse = custom_flash_attn.decode(_dev(q), _dev(kc), _dev(vc), sl, _dev(kn), _dev(vn), return_lse=True)
+    torch.cuda.synchronize()
+    kc[:, :, N_max - 1], vc[:, :, N_max - 1] = kn, vn
+    o_ref, l_ref = decode_np(q, kc, vc, [N_max] * B, 0.125)
+    _check(o, lse, o_ref, l_ref, "GPT-2-XL decode shape")
+
+
+def test_decode_argument_errors():
+    q = torch.zeros(1, 2, 64, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(1, 2, 16, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="needs cache_seqlens"):
+        custom_flash_attn.decode(q, kc, kc, None, q, q)
+    with pytest.raises(RuntimeError, match="together"):
+        custom_flash_attn.decode(q, kc, kc, None, q, None)
+    with pytest.raises(RuntimeError, match="int32"):
+        custom_flash_attn.decode(q, kc, kc, torch.zeros(1, dtype=torch.int64, device=DEV))
+    with pytest.raises(RuntimeError, match="q must have shape"):
+        custom_flash_attn.decode(q[:, :1], kc, kc)
+    padded = torch.zeros(1, 2, 16, 68, dtype=torch.bfloat16, device=DEV)[..., :64]  # 136 B rows
+    with pytest.raises(RuntimeError, match="unsupported strides"):
+        custom_flash_attn.decode(q, padded, padded)

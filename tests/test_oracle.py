@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from oracle import (
-    CONFIGS, attention_c, attention_np, bf16_bits_to_f32, bf16_round, f32_to_bf16_bits,
+    CONFIGS, attention_c, attention_np, bf16_bits_to_f32, bf16_round, decode_np, f32_to_bf16_bits,
     make_inputs, manual_attention_torch, sha256_bf16,
 )
 
@@ -255,3 +255,44 @@ def test_config_inputs_match_committed_hashes():
     # config 3 draws Q and K with sigma 3: their spread shows it.
     q, _, v = make_inputs(CONFIGS["config1"])
     assert 0.9 < q.std() < 1.1 and 0.9 < v.std() < 1.1
+
+
+# ------------------------------------------------------------------ decode step
+
+
+def test_decode_oracle_is_the_last_causal_row():
+    """decode_np(q, cache, L) must equal row L-1 of the causal forward over the first L
+    tokens, with q as that row's query (the value generate() keeps, model_inference.py:205)."""
+    B, H, N_max, D = 3, 2, 90, 64
+    kc, vc = _rand((B, H, N_max, D), 300, 3.0), _rand((B, H, N_max, D), 301)
+    q = _rand((B, H, D), 302, 3.0)
+    lens = [1, 57, 90]
+    o, lse = decode_np(q, kc, vc, lens, 0.125)
+    for b, L in enumerate(lens):
+        qf = _rand((1, H, L, D), 303 + b, 3.0)
+        qf[0, :, L - 1] = q[b]
+        of, lf = attention_np(qf, kc[b:b + 1, :, :L], vc[b:b + 1, :, :L], 0.125, True)
+        np.testing.assert_allclose(o[b], of[0, :, L - 1], rtol=0, atol=1e-12)
+        np.testing.assert_allclose(lse[b], lf[0, :, L - 1], rtol=0, atol=1e-12)
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            torch.from_numpy(q[b][:, None].astype(np.float64)),
+            torch.from_numpy(kc[b, :, :L].astype(np.float64)),
+            torch.from_numpy(vc[b, :, :L].astype(np.float64)), scale=0.125).numpy()[:, 0]
+        np.testing.assert_allclose(o[b], ref, rtol=0, atol=1e-12)
+
+
+def test_decode_oracle_empty_and_off_by_one():
+    B, H, N_max, D = 2, 2, 40, 64
+    kc, vc = _rand((B, H, N_max, D), 310, 2.0), _rand((B, H, N_max, D), 311)
+    q = _rand((B, H, D), 312, 2.0)
+    o, lse = decode_np(q, kc, vc, [0, 40])
+    assert (o[0] == 0).all() and np.isneginf(lse[0]).all()
+    # A length off by one either way must change the answer (the checks can see it).
+    o_m, _ = decode_np(q, kc, vc, [0, 39])
+    o_p, _ = decode_np(q, kc[:, :, :39], vc[:, :, :39], [0, 39])
+    np.testing.assert_array_equal(o_m, o_p)
+    assert np.abs(o_m[1] - o[1]).max() > 1e-3
+    # One key: the output is that key's value row, lse = scale * q.k.
+    o1, l1 = decode_np(q, kc, vc, [1, 1], 0.125)
+    np.testing.assert_allclose(o1, vc[:, :, 0], rtol=0, atol=1e-15)
+    np.testing.assert_allclose(l1, 0.125 * np.einsum("bhd,bhd->bh", q.astype(np.float64), kc[:, :, 0].astype(np.float64)), rtol=0, atol=1e-12)

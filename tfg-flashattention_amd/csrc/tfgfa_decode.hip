@@ -1,0 +1,475 @@
+// tfgfa_decode.hip - one decode step of attention over a KV cache, MI355X (gfx950), bf16.
+//
+// What it replaces: the reference's generate() has no KV cache; every new token re-runs the
+// whole prefix through the model, i.e. a full causal forward of which only the last query row
+// is kept (src/py/model_inference.py:199-228, timed at :444-457).  The last row of that causal
+// forward is exactly attention of one query over all cached keys:
+//     o = softmax_j(scale * q . k_j) v_j,  j < L,   lse = log sum_j exp(scale * q . k_j)
+// (the same math as model_inference.py:68-75 restricted to row L-1).  This file computes that
+// row directly from a cache, optionally appending the new token's k/v first.
+//
+// Bound: HBM.  Every cached K and V byte is read once (2 * 128 B per key per head) and the
+// arithmetic is 2 * 64 FMAs per key, about 0.5 FLOP/B, so the MFMA units have nothing to do:
+// scores and the P.V update are fp32 VALU FMAs on bf16 values widened in registers.
+//
+// Work decomposition (split over the cache sequence)
+//   grid = B * H * S workgroups; workgroup (bh, s) covers keys [s*C, s*C + C) of head bh.
+//   S and C are chosen on the host from N_max and the CU count so the grid fills the chip even
+//   at small B*H.  Inside a workgroup, wave w takes 32-key blocks w, w+4, w+8, ... of the chunk.
+//   Lane l of a wave handles keys (block + l/4) and (block + l/4 + 16), head dims 8c .. 8c+7
+//   and 32+8c .. 32+8c+7 (c = l%4): two buffer_load_dwordx4 per key row per lane, so a wave
+//   instruction reads 16 rows x 64 contiguous bytes.  The next block's K and V loads are
+//   issued before the current block is computed.
+//   Each quad of lanes (one key column of the wave) runs its own online softmax over its
+//   keys, so the only cross-lane step per block is the 2-step DPP sum of a dot product within
+//   the quad; columns, waves and (when S > 1) workgroups are merged once at the end with the
+//   log-sum-exp rule  o = sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i.
+//   S > 1: each workgroup writes its normalised partial (o_s, log2-domain lse_s) to the
+//   caller's workspace and decode_merge_kernel combines the S partials of a head.
+//   S = 1: the workgroup writes O and LSE itself.
+//
+// Cache append: with k_new/v_new given, key L_b = cache_seqlens[b] is the new token: the
+// workgroup whose chunk holds it stores k_new/v_new into cache row L_b and uses the values
+// from the inputs (no other workgroup reads that row), and attention covers L_b + 1 keys.
+// Loads of cache rows at or past L_b return zero (buffer range check, num_records = L_b rows),
+// so rows past the valid length are never read from memory.
+//
+// Invalid lengths (L_b < 0 or L_b + append > N_max) cannot be rejected before launch (they
+// live in device memory): for such a batch row the kernel writes NaN to O and LSE, reads no
+// key and appends nothing.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "tfgfa.h"
+
+namespace tfgfa_decode {
+
+constexpr int kD = 64;
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kWaveKeys = 32;                  // keys per wave per block
+constexpr int kBlockKeys = kWaves * kWaveKeys; // keys per workgroup per block (chunk granule)
+constexpr int kGroups = 16;                    // key columns per wave (4 lanes each)
+constexpr int kStreams = kWaves * kGroups;     // independent softmax streams per workgroup
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kPartFloats = kD + 1;            // per (head, split): o_s[64], lse_s
+// A buffer offset past any num_records this file builds (those stay below 2^31 - 2^24): the
+// load returns zero without a memory access.  Used for the prefetch after the last block.
+constexpr int kOutOfRange = 0x7FFFFFF0;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct Rows {  // element strides of a (B, H, N, 64) operand (last dim dense)
+  long long b, h, n;
+};
+struct Vecs {  // element strides of a (B, H, 64) operand
+  long long b, h;
+};
+
+// NaN marks results of invalid cache lengths.  The device pass is compiled with
+// -fno-honor-nans, under which a floating-point select may drop a NaN operand, so these
+// stores choose between bit patterns and write them through integer pointers.
+__device__ __forceinline__ void store_o(__bf16* p, float v, bool valid) {
+  const unsigned short bits = __builtin_bit_cast(unsigned short, (__bf16)v);
+  *reinterpret_cast<unsigned short*>(p) = valid ? bits : (unsigned short)0x7FC0;
+}
+__device__ __forceinline__ void store_lse(float* p, float v, bool valid) {
+  *reinterpret_cast<uint32_t*>(p) = valid ? __float_as_uint(v) : 0x7FC00000u;
+}
+
+__device__ __forceinline__ float bf_lo(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nbytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Sum over the 4 lanes of a key column (one quad): xor 1 and xor 2 by DPP quad permutations.
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+  return x;
+}
+
+// This lane's share of one 32-key block: keys key0 and key0 + 16 (r = 0, 1), each as two
+// 16-byte pieces: dims 8c .. 8c+7 (piece 0, bytes 16c) and 32+8c .. +7 (piece 1, bytes
+// 64+16c).  A wave instruction reads 16 rows x 64 contiguous bytes.
+struct KV {
+  u32x4 k[2][2], v[2][2];
+};
+
+// kb: the block's first key (wave-uniform); k_lane/v_lane: this lane's byte offsets within a
+// block, (l/4 + 16r) * row + 16c.  A block that is not live loads from kOutOfRange (+ the
+// lane part, still past num_records as an unsigned 32-bit offset).
+__device__ __forceinline__ void load_block(KV& x, __amdgpu_buffer_rsrc_t kd,
+                                           __amdgpu_buffer_rsrc_t vd, int krow, int vrow, int kb,
+                                           bool live, const int (&k_lane)[2],
+                                           const int (&v_lane)[2]) {
+  const int ks = __builtin_amdgcn_readfirstlane(live ? kb * krow : kOutOfRange);
+  const int vs = __builtin_amdgcn_readfirstlane(live ? kb * vrow : kOutOfRange);
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      x.k[r][p] = load16(kd, ks + k_lane[r] + 64 * p);
+      x.v[r][p] = load16(vd, vs + v_lane[r] + 64 * p);
+    }
+}
+
+// Online-softmax update of this key column's stream (m, l, o[16]) with the block's 2 keys.
+__device__ __forceinline__ void block_update(const KV& x, const float (&qf)[16], int key0,
+                                             int key_end, float& m, float& l, float (&o)[16]) {
+  float s[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc0 = fmaf(qf[2 * i], bf_lo(x.k[r][0][i]), acc0);
+      acc0 = fmaf(qf[2 * i + 1], bf_hi(x.k[r][0][i]), acc0);
+      acc1 = fmaf(qf[8 + 2 * i], bf_lo(x.k[r][1][i]), acc1);
+      acc1 = fmaf(qf[8 + 2 * i + 1], bf_hi(x.k[r][1][i]), acc1);
+    }
+    const float acc = quad_sum(acc0 + acc1);
+    s[r] = (key0 + 16 * r < key_end) ? acc : -INFINITY;
+  }
+  const float m_new = fmaxf(m, fmaxf(s[0], s[1]));
+  const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+  const float alpha = exp2f(m - m_use);
+  const float p0 = exp2f(s[0] - m_use), p1 = exp2f(s[1] - m_use);
+  l = fmaf(l, alpha, p0 + p1);
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float a = o[8 * p + 2 * i] * alpha, b = o[8 * p + 2 * i + 1] * alpha;
+      a = fmaf(p0, bf_lo(x.v[0][p][i]), a);
+      b = fmaf(p0, bf_hi(x.v[0][p][i]), b);
+      a = fmaf(p1, bf_lo(x.v[1][p][i]), a);
+      b = fmaf(p1, bf_hi(x.v[1][p][i]), b);
+      o[8 * p + 2 * i] = a;
+      o[8 * p + 2 * i + 1] = b;
+    }
+  m = m_new;
+}
+
+// The new token's row replaces the (zero-filled) loads of cache row Lc in the block that
+// holds it.
+__device__ __forceinline__ void put_new(KV& x, int key0, int Lc, const u32x4 (&kn)[2],
+                                        const u32x4 (&vn)[2]) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    if (key0 + 16 * r == Lc) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        x.k[r][p] = kn[p];
+        x.v[r][p] = vn[p];
+      }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void decode_kernel(
+    const __bf16* __restrict__ Q, Vecs qs, __bf16* Kc, Rows ks, __bf16* Vc, Rows vs,
+    const __bf16* __restrict__ Kn, Vecs kns, const __bf16* __restrict__ Vn, Vecs vns,
+    const int* __restrict__ seqlens, __bf16* __restrict__ O, Vecs os, float* __restrict__ LSE,
+    float* __restrict__ part, int H, int N_max, int S, int C, float scale_log2) {
+  __shared__ float sh_o[kStreams][kD];
+  __shared__ float sh_m[kStreams], sh_l[kStreams];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 2;  // key column within the wave
+  const int c = lane & 3;   // dims 8c .. 8c+7 and 32+8c .. 32+8c+7
+
+  const int bh = blockIdx.x / S;
+  const int s = blockIdx.x - bh * S;
+  const int b = bh / H, h = bh - b * H;
+  const bool append = Kn != nullptr;
+
+  const int Lc = seqlens ? seqlens[b] : N_max;  // valid cached rows
+  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
+  const int L = valid ? Lc + (append ? 1 : 0) : 0;  // keys attended
+  const int c0 = s * C;
+  const int c1 = min(c0 + C, L);
+
+  __bf16* Kh = Kc + b * ks.b + h * ks.h;
+  __bf16* Vh = Vc + b * vs.b + h * vs.h;
+  const int krow = (int)ks.n * 2, vrow = (int)vs.n * 2;
+  const int Lr = valid ? Lc : 0;
+  const __amdgpu_buffer_rsrc_t kd = rows_rsrc(Kh, Lr * krow);
+  const __amdgpu_buffer_rsrc_t vd = rows_rsrc(Vh, Lr * vrow);
+
+  // The new token: stored into the cache by the workgroup whose chunk holds row Lc.
+  u32x4 k_app[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, v_app[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+  const bool has_new = append && valid && Lc >= c0 && Lc < c0 + C;
+  if (has_new) {
+    const __bf16* kn = Kn + b * kns.b + h * kns.h;
+    const __bf16* vn = Vn + b * vns.b + h * vns.h;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      k_app[p] = *reinterpret_cast<const u32x4*>(kn + 32 * p + 8 * c);
+      v_app[p] = *reinterpret_cast<const u32x4*>(vn + 32 * p + 8 * c);
+    }
+    if (wave == 0 && g == 0) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        *reinterpret_cast<u32x4*>(Kh + (long long)Lc * ks.n + 32 * p + 8 * c) = k_app[p];
+        *reinterpret_cast<u32x4*>(Vh + (long long)Lc * vs.n + 32 * p + 8 * c) = v_app[p];
+      }
+    }
+  }
+
+  float qf[16];
+  {
+    const __bf16* qh = Q + b * qs.b + h * qs.h;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const u32x4 qv = *reinterpret_cast<const u32x4*>(qh + 32 * p + 8 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        qf[8 * p + 2 * i] = bf_lo(qv[i]) * scale_log2;
+        qf[8 * p + 2 * i + 1] = bf_hi(qv[i]) * scale_log2;
+      }
+    }
+  }
+
+  float m = -INFINITY, l = 0.f, o[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = 0.f;
+
+  // Blocks of this wave: kb = c0 + 32*wave + 128*t.  Two register sets used in turn, so the
+  // next block's loads are in flight while the current one is computed, with no copies
+  // between the sets (a copy would wait for the loads).
+  int kb = c0 + wave * kWaveKeys;
+  if (kb < c1) {
+    const int nblk = (c1 - kb + kBlockKeys - 1) / kBlockKeys;  // this wave's blocks
+    const int k_lane[2] = {g * krow + 16 * c, (g + 16) * krow + 16 * c};
+    const int v_lane[2] = {g * vrow + 16 * c, (g + 16) * vrow + 16 * c};
+    KV A, B;
+    load_block(A, kd, vd, krow, vrow, kb, true, k_lane, v_lane);
+    // Pairs of blocks with one back edge and no exit inside the body: at the top of an
+    // iteration only A's loads are outstanding.
+    for (int t = 0; t + 2 <= nblk; t += 2) {
+      load_block(B, kd, vd, krow, vrow, kb + kBlockKeys, true, k_lane, v_lane);
+      if (has_new && Lc >= kb && Lc < kb + kWaveKeys) put_new(A, kb + g, Lc, k_app, v_app);
+      block_update(A, qf, kb + g, c1, m, l, o);
+      kb += kBlockKeys;
+      load_block(A, kd, vd, krow, vrow, kb + kBlockKeys, t + 2 < nblk, k_lane, v_lane);
+      if (has_new && Lc >= kb && Lc < kb + kWaveKeys) put_new(B, kb + g, Lc, k_app, v_app);
+      block_update(B, qf, kb + g, c1, m, l, o);
+      kb += kBlockKeys;
+    }
+    if (nblk & 1) {
+      if (has_new && Lc >= kb && Lc < kb + kWaveKeys) put_new(A, kb + g, Lc, k_app, v_app);
+      block_update(A, qf, kb + g, c1, m, l, o);
+    }
+  }
+
+  // Merge the 64 streams of the workgroup (16 key columns x 4 waves) in LDS.
+  const int stream = wave * kGroups + g;
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sh_o[stream][32 * p + 8 * c + i] = o[8 * p + i];
+  if (c == 0) {
+    sh_m[stream] = m;
+    sh_l[stream] = l;
+  }
+  __syncthreads();
+  if (tid >= kD) return;
+  const int d = tid;
+  float M = -INFINITY;
+#pragma unroll 8
+  for (int i = 0; i < kStreams; ++i) M = fmaxf(M, sh_m[i]);
+  const float M_use = (M == -INFINITY) ? 0.f : M;
+  float lt = 0.f, ot = 0.f;
+#pragma unroll 8
+  for (int i = 0; i < kStreams; ++i) {
+    const float w = exp2f(sh_m[i] - M_use);
+    lt = fmaf(w, sh_l[i], lt);
+    ot = fmaf(w, sh_o[i][d], ot);
+  }
+  const float on = lt > 0.f ? ot / lt : 0.f;
+  const float lse2 = lt > 0.f ? M + log2f(lt) : -INFINITY;
+  if (S == 1) {
+    store_o(O + b * os.b + h * os.h + d, on, valid);
+    if (LSE != nullptr && d == 0) store_lse(LSE + bh, lse2 * kLn2, valid);
+  } else {
+    float* pp = part + ((long long)bh * S + s) * kPartFloats;
+    pp[d] = on;
+    if (d == 0) pp[kD] = lse2;
+  }
+}
+
+// Combines the S partials of each head: one wave per head, lane = head dim.
+__global__ __launch_bounds__(kThreads) void decode_merge_kernel(
+    const float* __restrict__ part, const int* __restrict__ seqlens, __bf16* __restrict__ O,
+    Vecs os, float* __restrict__ LSE, int BH, int H, int N_max, int S, bool append) {
+  const int bh = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (bh >= BH) return;
+  const int d = threadIdx.x & 63;
+  const int b = bh / H, h = bh - b * H;
+  const int Lc = seqlens ? seqlens[b] : N_max;
+  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
+  const float* p = part + (long long)bh * S * kPartFloats;
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, p[s * kPartFloats + kD]);
+  const float M_use = (M == -INFINITY) ? 0.f : M;
+  float wt = 0.f, ot = 0.f;
+  for (int s = 0; s < S; ++s) {
+    const float w = exp2f(p[s * kPartFloats + kD] - M_use);
+    wt += w;
+    ot = fmaf(w, p[s * kPartFloats + d], ot);
+  }
+  const float on = wt > 0.f ? ot / wt : 0.f;
+  store_o(O + b * os.b + h * os.h + d, on, valid);
+  if (LSE != nullptr && d == 0)
+    store_lse(LSE + bh, wt > 0.f ? (M + log2f(wt)) * kLn2 : -INFINITY, valid);
+}
+
+// ---------------------------------------------------------------------------------------
+// Host side.
+
+// Splits for a cache of N_max rows: enough workgroups for two per CU, chunks a multiple of
+// kBlockKeys, no empty split.
+static void choose_split(int BH, int N_max, int cu_count, int max_splits, int* S_out, int* C_out) {
+  const int blocks = std::max(1, (N_max + kBlockKeys - 1) / kBlockKeys);
+  int S = std::max(1, (2 * cu_count + BH - 1) / BH);
+  S = std::min(S, blocks);
+  S = std::max(1, std::min(S, max_splits));
+  const int C = (blocks + S - 1) / S * kBlockKeys;
+  S = std::max(1, (N_max + C - 1) / C);
+  *S_out = S;
+  *C_out = C;
+}
+
+static bool rows_ok(const int64_t* st, int B, int H, int N_max, Rows* out) {
+  Rows r;
+  r.b = B == 1 ? 0 : st[0];
+  r.h = H == 1 ? 0 : st[1];
+  r.n = N_max <= 1 ? kD : st[2];
+  if (st[3] != 1) return false;
+  if (r.b < 0 || r.h < 0 || r.n < kD || ((r.b | r.h | r.n) & 7)) return false;
+  *out = r;
+  return true;
+}
+
+static bool vecs_ok(const int64_t* st, int B, int H, Vecs* out) {
+  Vecs v;
+  v.b = B == 1 ? 0 : st[0];
+  v.h = H == 1 ? 0 : st[1];
+  if (st[2] != 1) return false;
+  if (v.b < 0 || v.h < 0 || ((v.b | v.h) & 7)) return false;
+  *out = v;
+  return true;
+}
+
+// O rows (64 elements each) must not share elements: sorted by stride, each stride of a
+// dimension of size > 1 is at least the span reached through the smaller one.
+static bool vecs_overlap(const Vecs& v, int B, int H) {
+  long long st[2] = {v.b, v.h}, sz[2] = {B, H};
+  if (st[1] < st[0]) {
+    const long long t = st[0], z = sz[0];
+    st[0] = st[1];
+    sz[0] = sz[1];
+    st[1] = t;
+    sz[1] = z;
+  }
+  long long reach = kD - 1;
+  for (int i = 0; i < 2; ++i) {
+    if (sz[i] == 1) continue;
+    if (st[i] <= reach) return true;
+    reach += (sz[i] - 1) * st[i];
+  }
+  return false;
+}
+
+}  // namespace tfgfa_decode
+
+extern "C" size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max) {
+  using namespace tfgfa_decode;
+  if (B <= 0 || H <= 0 || N_max <= 0) return 0;
+  const size_t blocks = ((size_t)N_max + kBlockKeys - 1) / kBlockKeys;
+  return (size_t)B * (size_t)H * blocks * kPartFloats * sizeof(float);
+}
+
+extern "C" int tfgfa_decode_bf16(const void* q, const int64_t* q_strides, void* k_cache,
+                                 const int64_t* k_strides, void* v_cache,
+                                 const int64_t* v_strides, const void* k_new,
+                                 const int64_t* k_new_strides, const void* v_new,
+                                 const int64_t* v_new_strides, const int* cache_seqlens, void* o,
+                                 const int64_t* o_strides, float* lse, int B, int H, int N_max,
+                                 int D, float softmax_scale, void* workspace,
+                                 size_t workspace_bytes, void* hip_stream) {
+  using namespace tfgfa_decode;
+  if (B < 0 || H < 0 || N_max < 0) return TFGFA_ERR_BAD_SHAPE;
+  if (D != kD) return TFGFA_ERR_HEAD_DIM;
+  if (!(softmax_scale > 0.f) || !isfinite(softmax_scale)) return TFGFA_ERR_SCALE;
+  if ((k_new == nullptr) != (v_new == nullptr)) return TFGFA_ERR_NULL_POINTER;
+  const bool append = k_new != nullptr;
+  if (append && cache_seqlens == nullptr) return TFGFA_ERR_CACHE;
+  if (B == 0 || H == 0) return TFGFA_OK;
+  const long long bh = (long long)B * H;
+  if (bh > INT32_MAX / 64) return TFGFA_ERR_TOO_LARGE;
+
+  Rows ks, vs;
+  Vecs qs, os, kns = {0, 0}, vns = {0, 0};
+  if (!q_strides || !k_strides || !v_strides || !o_strides) return TFGFA_ERR_NULL_POINTER;
+  if (append && (!k_new_strides || !v_new_strides)) return TFGFA_ERR_NULL_POINTER;
+  if (!vecs_ok(q_strides, B, H, &qs) || !vecs_ok(o_strides, B, H, &os)) return TFGFA_ERR_STRIDE;
+  if (!rows_ok(k_strides, B, H, N_max, &ks) || !rows_ok(v_strides, B, H, N_max, &vs))
+    return TFGFA_ERR_STRIDE;
+  if (append && (!vecs_ok(k_new_strides, B, H, &kns) || !vecs_ok(v_new_strides, B, H, &vns)))
+    return TFGFA_ERR_STRIDE;
+  if (vecs_overlap(os, B, H)) return TFGFA_ERR_STRIDE;
+  // Cache rows are addressed with 32-bit buffer offsets (row index * row stride, plus a block).
+  if (((long long)N_max + kBlockKeys) * ks.n * 2 > INT32_MAX ||
+      ((long long)N_max + kBlockKeys) * vs.n * 2 > INT32_MAX)
+    return TFGFA_ERR_TOO_LARGE;
+
+  if (!q || !k_cache || !v_cache || !o) return TFGFA_ERR_NULL_POINTER;
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)o |
+       (uintptr_t)k_new | (uintptr_t)v_new | (uintptr_t)workspace) & 15u)
+    return TFGFA_ERR_ALIGNMENT;
+  if (((uintptr_t)lse | (uintptr_t)cache_seqlens) & 3u) return TFGFA_ERR_ALIGNMENT;
+
+  int cu = 0;
+  const int st = tfgfa_device_info(&cu, nullptr, nullptr, 0);
+  if (st != TFGFA_OK) return st;
+  const size_t per_split = (size_t)bh * kPartFloats * sizeof(float);
+  const int ws_splits =
+      workspace ? (int)std::min((size_t)INT32_MAX, workspace_bytes / per_split) : 0;
+  int S, C;
+  choose_split((int)bh, N_max, cu, std::max(1, ws_splits), &S, &C);
+  if (bh * S > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
+
+  const hipStream_t stream = (hipStream_t)hip_stream;
+  const float scale_log2 = softmax_scale * kLog2e;
+  hipLaunchKernelGGL(decode_kernel, dim3((unsigned)(bh * S)), dim3(kThreads), 0, stream,
+                     static_cast<const __bf16*>(q), qs, static_cast<__bf16*>(k_cache), ks,
+                     static_cast<__bf16*>(v_cache), vs, static_cast<const __bf16*>(k_new), kns,
+                     static_cast<const __bf16*>(v_new), vns, cache_seqlens,
+                     static_cast<__bf16*>(o), os, lse, static_cast<float*>(workspace), H, N_max,
+                     S, C, scale_log2);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return -(int)e;
+  if (S > 1) {
+    hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((bh + kWaves - 1) / kWaves)),
+                       dim3(kThreads), 0, stream, static_cast<const float*>(workspace),
+                       cache_seqlens, static_cast<__bf16*>(o), os, lse, (int)bh, H, N_max, S,
+                       append);
+    e = hipGetLastError();
+    if (e != hipSuccess) return -(int)e;
+  }
+  return TFGFA_OK;
+}

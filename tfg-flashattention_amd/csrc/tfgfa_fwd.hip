@@ -701,6 +701,7 @@ extern "C" const char* tfgfa_strerror(int status) {
     case TFGFA_ERR_CAUSAL_FLAG: return "causal flag must be 0 or 1";
     case TFGFA_ERR_TOO_LARGE: return "problem exceeds the launch limits (B*H*ceil(N/128) < 2^31)";
     case TFGFA_ERR_ALIGNMENT: return "misaligned pointer (q/k/v/o need 16 B, lse 4 B)";
+    case TFGFA_ERR_CACHE: return "k_new/v_new (cache append) need cache_seqlens";
     case TFGFA_ERR_STRIDE:
       return "unsupported strides (last dim 1; b, h, n non-negative multiples of 8; n >= 64; "
              "o without overlapping elements)";

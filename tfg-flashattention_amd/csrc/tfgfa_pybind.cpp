@@ -57,6 +57,31 @@ void fwd_strided(std::uintptr_t q, const Strides4& qs, std::uintptr_t k, const S
   }
 }
 
+using Strides3 = std::array<std::int64_t, 3>;
+
+void decode(std::uintptr_t q, const Strides3& qs, std::uintptr_t kc, const Strides4& ks,
+            std::uintptr_t vc, const Strides4& vs, std::uintptr_t kn, const Strides3& kns,
+            std::uintptr_t vn, const Strides3& vns, std::uintptr_t seqlens, std::uintptr_t o,
+            const Strides3& os, std::uintptr_t lse, int B, int H, int N_max, int D,
+            float softmax_scale, std::uintptr_t workspace, std::size_t workspace_bytes,
+            std::uintptr_t stream) {
+  int st;
+  {
+    py::gil_scoped_release nogil;
+    st = tfgfa_decode_bf16(
+        reinterpret_cast<const void*>(q), qs.data(), reinterpret_cast<void*>(kc), ks.data(),
+        reinterpret_cast<void*>(vc), vs.data(), reinterpret_cast<const void*>(kn), kns.data(),
+        reinterpret_cast<const void*>(vn), vns.data(), reinterpret_cast<const int*>(seqlens),
+        reinterpret_cast<void*>(o), os.data(), reinterpret_cast<float*>(lse), B, H, N_max, D,
+        softmax_scale, reinterpret_cast<void*>(workspace), workspace_bytes,
+        reinterpret_cast<void*>(stream));
+  }
+  if (st != TFGFA_OK) {
+    throw std::runtime_error(std::string("tfgfa_decode_bf16 failed (status ") +
+                             std::to_string(st) + "): " + tfgfa_strerror(st));
+  }
+}
+
 py::dict device_info() {
   int cu = 0, mhz = 0;
   char arch[128] = {0};
@@ -85,6 +110,17 @@ PYBIND11_MODULE(_C, m) {
         py::arg("v_strides"), py::arg("o"), py::arg("o_strides"), py::arg("lse"), py::arg("B"),
         py::arg("H"), py::arg("N"), py::arg("D"), py::arg("softmax_scale"), py::arg("causal"),
         py::arg("stream"));
+  m.def("decode", &decode,
+        "One decode step over a KV cache on raw device pointers (element strides)",
+        py::arg("q"), py::arg("q_strides"), py::arg("k_cache"), py::arg("k_strides"),
+        py::arg("v_cache"), py::arg("v_strides"), py::arg("k_new"), py::arg("k_new_strides"),
+        py::arg("v_new"), py::arg("v_new_strides"), py::arg("cache_seqlens"), py::arg("o"),
+        py::arg("o_strides"), py::arg("lse"), py::arg("B"), py::arg("H"), py::arg("N_max"),
+        py::arg("D"), py::arg("softmax_scale"), py::arg("workspace"),
+        py::arg("workspace_bytes"), py::arg("stream"));
+  m.def("decode_workspace_bytes", [](int B, int H, int N_max) {
+    return tfgfa_decode_workspace_bytes(B, H, N_max);
+  });
   m.def("device_info", &device_info, "CU count, shader clock (MHz) and arch of the current device");
   m.def("strerror", [](int st) { return std::string(tfgfa_strerror(st)); });
   m.def("abi_version", []() { return tfgfa_abi_version(); });

@@ -30,7 +30,8 @@ except ImportError as exc:  # pragma: no cover - exercised only on a broken buil
         f"({exc}); run `make -C tfg-flashattention_amd/csrc` or __graft_entry__.build()"
     ) from exc
 
-__all__ = ["forward", "forward_lse", "attention", "device_info", "HEAD_DIM", "library_path"]
+__all__ = ["forward", "forward_lse", "attention", "decode", "device_info", "HEAD_DIM",
+           "library_path"]
 
 HEAD_DIM = 64  # the only compiled head dimension (common_types.hpp:33 fixes K = 64 too)
 
@@ -162,6 +163,94 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, out: torch.T
             q.data_ptr(), q.stride(), k.data_ptr(), k.stride(), v.data_ptr(), v.stride(),
             out.data_ptr(), out.stride(), 0 if lse is None else lse.data_ptr(),
             B, H, N, D, scale, bool(causal), stream,
+        )
+    return (out, lse) if return_lse else out
+
+
+def _check_vec(x, name: str, B: int, H: int, dev) -> None:
+    if not x.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if x.dtype != torch.bfloat16:
+        raise RuntimeError("Unsupported tensor dtype. Use bfloat16.")
+    if tuple(x.shape) != (B, H, HEAD_DIM):
+        raise RuntimeError(f"{name} must have shape {(B, H, HEAD_DIM)}, got {tuple(x.shape)}")
+    if x.device != dev:
+        raise RuntimeError(f"{name} must be on {dev}, got {x.device}")
+    if x.stride(2) != 1:
+        raise RuntimeError(f"{name} must be dense in its last dimension (stride 1), got strides {x.stride()}")
+
+
+def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+           cache_seqlens: torch.Tensor | None = None, k_new: torch.Tensor | None = None,
+           v_new: torch.Tensor | None = None, *, out: torch.Tensor | None = None,
+           softmax_scale: float | None = None, return_lse: bool = False,
+           workspace: torch.Tensor | None = None):
+    """One decode step: attention of one new query per (batch, head) over a KV cache.
+
+    ``q``: (B, H, 64) bf16.  ``k_cache``, ``v_cache``: (B, H, N_max, 64) bf16 views (any
+    strides with a dense last dimension, e.g. (B, N_max, H, 64) buffers transposed).
+    ``cache_seqlens``: int32 (B,) on the device, the number of valid cached rows per batch
+    row (``None``: all N_max rows).  With ``k_new``/``v_new`` ((B, H, 64) bf16) the new token is
+    written into cache row ``cache_seqlens[b]`` first and attended too; the caller advances
+    ``cache_seqlens`` afterwards.  Returns ``out`` ((B, H, 64), new if not given), or
+    ``(out, lse)`` with ``return_lse=True`` (lse (B, H) float32, natural log).  The result
+    equals the last row of the causal forward over the first L tokens - what the reference's
+    generate() recomputes from scratch for every token (src/py/model_inference.py:199-228).
+    A length that does not fit the cache yields NaN for that batch row (checked on the device).
+    ``workspace``: optional uint8 device buffer for split-sequence partials; one of
+    ``_C.decode_workspace_bytes(B, H, N_max)`` bytes is allocated per call when absent.
+    """
+    for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        if not t.is_cuda:
+            raise RuntimeError(f"{n} must be a CUDA tensor")
+        if t.dtype != torch.bfloat16:
+            raise RuntimeError("Unsupported tensor dtype. Use bfloat16.")
+        if t.dim() != 4 or t.shape[3] != HEAD_DIM:
+            raise RuntimeError(f"{n} must be (B, H, N_max, {HEAD_DIM}), got {tuple(t.shape)}")
+        if t.stride(3) != 1:
+            raise RuntimeError(f"{n} must be dense in its last dimension (stride 1), got strides {t.stride()}")
+    B, H, N_max, D = k_cache.shape
+    if v_cache.shape != k_cache.shape:
+        raise RuntimeError(f"v_cache must have shape {tuple(k_cache.shape)}, got {tuple(v_cache.shape)}")
+    dev = k_cache.device
+    if v_cache.device != dev:
+        raise RuntimeError(f"v_cache must be on {dev}, got {v_cache.device}")
+    _check_vec(q, "q", B, H, dev)
+    if (k_new is None) != (v_new is None):
+        raise RuntimeError("k_new and v_new must be given together")
+    if k_new is not None:
+        _check_vec(k_new, "k_new", B, H, dev)
+        _check_vec(v_new, "v_new", B, H, dev)
+        if cache_seqlens is None:
+            raise RuntimeError("appending k_new/v_new needs cache_seqlens")
+    if cache_seqlens is not None:
+        if cache_seqlens.dtype != torch.int32 or tuple(cache_seqlens.shape) != (B,):
+            raise RuntimeError(f"cache_seqlens must be int32 of shape ({B},)")
+        if cache_seqlens.device != dev or not cache_seqlens.is_contiguous():
+            raise RuntimeError(f"cache_seqlens must be a contiguous tensor on {dev}")
+    if out is None:
+        out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
+    else:
+        _check_vec(out, "out", B, H, dev)
+    scale = (1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
+    lse = torch.empty((B, H), dtype=torch.float32, device=dev) if return_lse else None
+    if workspace is None:
+        workspace = torch.empty(_C.decode_workspace_bytes(B, H, N_max), dtype=torch.uint8, device=dev)
+    elif not workspace.is_cuda or workspace.device != dev or not workspace.is_contiguous():
+        raise RuntimeError(f"workspace must be a contiguous tensor on {dev}")
+    zero3 = (0, 0, 0)
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _C.decode(
+            q.data_ptr(), q.stride(), k_cache.data_ptr(), k_cache.stride(),
+            v_cache.data_ptr(), v_cache.stride(),
+            0 if k_new is None else k_new.data_ptr(), zero3 if k_new is None else k_new.stride(),
+            0 if v_new is None else v_new.data_ptr(), zero3 if v_new is None else v_new.stride(),
+            0 if cache_seqlens is None else cache_seqlens.data_ptr(),
+            out.data_ptr(), out.stride(), 0 if lse is None else lse.data_ptr(),
+            B, H, N_max, D, scale,
+            workspace.data_ptr() if workspace.numel() else 0,
+            workspace.numel() * workspace.element_size(), stream,
         )
     return (out, lse) if return_lse else out
 
