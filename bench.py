@@ -13,6 +13,7 @@ Prints one JSON line.  ``value`` is TFLOP/s with the FlashAttention causal conve
 src/py/model_inference.py:68-75) on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 2000] [--no-cpu-baseline] [--no-strided]
+                      [--no-decode]
 """
 import argparse
 import json
@@ -132,6 +133,69 @@ def time_strided_views(dev, steps, warmup):
             "unit": "TFLOP/s", "steps": steps}
 
 
+DEC_SETS = 6  # 6 x 52 MB of K/V cache: more than the 256 MB Infinity Cache
+
+
+def decode_bytes(b=B, h=H, n=N, d=D):
+    """Algorithmic HBM bytes of one decode step with append at row n-1: K and V rows 0..n-2 read
+    from the cache (the new row comes from k_new/v_new), q, k_new, v_new read, the new K/V row
+    and O written (bf16), LSE written (fp32)."""
+    return b * h * (2 * (n - 1) * d * 2 + 3 * d * 2 + 2 * d * 2 + d * 2 + 4)
+
+
+def time_decode(dev, steps, warmup):
+    """One decode step of attention at the GPT-2-XL shape: B=8, H=25, a 1024-row KV cache per
+    head with 1023 valid rows, the new token appended (row 1023) and attended, O and LSE written.
+    The step is HBM-bound: the figure of merit is GB/s against the 8 TB/s HBM peak."""
+    import torch
+
+    from custom_flash_attn import _C
+
+    gen = torch.Generator(device=dev).manual_seed(4003)
+    sets = []
+    for _ in range(DEC_SETS):
+        kc = (torch.randn(B, H, N, D, device=dev, generator=gen) * SIGMA_QK).to(torch.bfloat16)
+        vc = torch.randn(B, H, N, D, device=dev, generator=gen).to(torch.bfloat16)
+        q, kn, vn = ((torch.randn(B, H, D, device=dev, generator=gen) * s).to(torch.bfloat16)
+                     for s in (SIGMA_QK, SIGMA_QK, SIGMA_V))
+        sets.append((q, kc, vc, kn, vn))
+    seqlens = torch.full((B,), N - 1, dtype=torch.int32, device=dev)
+    o = torch.empty(B, H, D, device=dev, dtype=torch.bfloat16)
+    lse = torch.empty(B, H, device=dev, dtype=torch.float32)
+    ws_bytes = _C.decode_workspace_bytes(B, H, N)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def step(i):
+        q, kc, vc, kn, vn = sets[i % DEC_SETS]
+        _C.decode(q.data_ptr(), q.stride(), kc.data_ptr(), kc.stride(), vc.data_ptr(), vc.stride(),
+                  kn.data_ptr(), kn.stride(), vn.data_ptr(), vn.stride(), seqlens.data_ptr(),
+                  o.data_ptr(), o.stride(), lse.data_ptr(), B, H, N, D, SCALE, ws.data_ptr(),
+                  ws_bytes, sh)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        step(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    gbs = decode_bytes() / (ms * 1e-3) / 1e9
+    return {
+        "workload": f"decode step, B={B} H={H} d={D}, cache {N} rows ({N - 1} valid + 1 appended), "
+                    f"O + LSE, {DEC_SETS} rotating caches",
+        "ms_per_step": round(ms, 5), "steps": steps,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "algorithmic_bytes": decode_bytes()},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -141,6 +205,8 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the decode-step leg (KV-cache attention, HBM-bound)")
     ap.add_argument("--no-strided", action="store_true",
                     help="skip the second timing of the same workload on strided (B, N, H, 64) views")
     ap.add_argument("--cpu-heads", type=int, default=200,
@@ -244,6 +310,8 @@ def main():
     }
     if not args.no_strided:
         result["strided_gpt2_views"] = time_strided_views(dev, max(1, args.steps // 2), max(1, args.warmup // 2))
+    if not args.no_decode:
+        result["decode"] = time_decode(dev, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         nh = max(1, min(args.cpu_heads, B * H))
         q, k, v, o = (t.reshape(1, B * H, N, D)[:, :nh] for t in sets[0][:4])

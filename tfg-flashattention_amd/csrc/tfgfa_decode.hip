@@ -9,28 +9,32 @@
 // row directly from a cache, optionally appending the new token's k/v first.
 //
 // Bound: HBM.  Every cached K and V byte is read once (2 * 128 B per key per head) and the
-// arithmetic is 2 * 64 FMAs per key, about 0.5 FLOP/B, so the MFMA units have nothing to do:
-// scores and the P.V update are fp32 VALU FMAs on bf16 values widened in registers.
+// arithmetic is 2 * 64 MACs per key, about 0.5 FLOP/B, so the MFMA units have nothing to do:
+// scores and the P.V update are VALU v_dot2_f32_bf16 on the bf16 values as loaded (two MACs
+// per instruction, fp32 accumulate), which keeps the VALU time per byte below the HBM time.
 //
 // Work decomposition (split over the cache sequence)
-//   grid = B * H * S workgroups; workgroup (bh, s) covers keys [s*C, s*C + C) of head bh.
-//   S and C are chosen on the host from N_max and the CU count so the grid fills the chip even
-//   at small B*H.  Inside a workgroup, wave w takes 32-key blocks w, w+4, w+8, ... of the chunk.
+//   grid = B * H * S workgroups of 8 waves; workgroup (bh, s) covers keys [s*C, s*C + C) of
+//   head bh.  S = 1 while B*H covers at least half the CUs; below that S and C are chosen on
+//   the host so the grid fills the chip.  Inside a workgroup, wave w takes 32-key blocks
+//   w, w+8, w+16, ... of the chunk.
 //   Lane l of a wave handles keys (block + l/4) and (block + l/4 + 16), head dims 8c .. 8c+7
 //   and 32+8c .. 32+8c+7 (c = l%4): two buffer_load_dwordx4 per key row per lane, so a wave
 //   instruction reads 16 rows x 64 contiguous bytes.  The next block's K and V loads are
 //   issued before the current block is computed.
 //   Each quad of lanes (one key column of the wave) runs its own online softmax over its
 //   keys, so the only cross-lane step per block is the 2-step DPP sum of a dot product within
-//   the quad; columns, waves and (when S > 1) workgroups are merged once at the end with the
-//   log-sum-exp rule  o = sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i.
+//   the quad; the 128 streams of a workgroup (in LDS) and, when S > 1, the workgroups are
+//   merged once at the end with the log-sum-exp rule
+//   o = sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i.
 //   S > 1: each workgroup writes its normalised partial (o_s, log2-domain lse_s) to the
 //   caller's workspace and decode_merge_kernel combines the S partials of a head.
 //   S = 1: the workgroup writes O and LSE itself.
 //
 // Cache append: with k_new/v_new given, key L_b = cache_seqlens[b] is the new token: the
-// workgroup whose chunk holds it stores k_new/v_new into cache row L_b and uses the values
-// from the inputs (no other workgroup reads that row), and attention covers L_b + 1 keys.
+// workgroup whose chunk holds it stores k_new/v_new into cache row L_b and folds the values
+// from the inputs into one softmax stream (no workgroup reads that row from the cache), and
+// attention covers L_b + 1 keys.
 // Loads of cache rows at or past L_b return zero (buffer range check, num_records = L_b rows),
 // so rows past the valid length are never read from memory.
 //
@@ -49,20 +53,25 @@
 namespace tfgfa_decode {
 
 constexpr int kD = 64;
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
-constexpr int kWaveKeys = 32;                  // keys per wave per block
+constexpr int kThreads = 512;
+constexpr int kWaves = 8;
+constexpr int kKeysPerLane = 2;                // keys per lane per block (rows 16 apart)
+static_assert(kKeysPerLane % 2 == 0, "P.V pairs keys");
+constexpr int kWaveKeys = 16 * kKeysPerLane;   // keys per wave per block
 constexpr int kBlockKeys = kWaves * kWaveKeys; // keys per workgroup per block (chunk granule)
 constexpr int kGroups = 16;                    // key columns per wave (4 lanes each)
-constexpr int kStreams = kWaves * kGroups;     // independent softmax streams per workgroup
+constexpr int kMergeThreads = 256;             // decode_merge_kernel: one wave per head
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kPartFloats = kD + 1;            // per (head, split): o_s[64], lse_s
+constexpr int kWorkspaceRows = 128;            // cache rows per split counted by the workspace
+static_assert(kBlockKeys % kWorkspaceRows == 0, "splits must not outnumber workspace slots");
 // A buffer offset past any num_records this file builds (those stay below 2^31 - 2^24): the
 // load returns zero without a memory access.  Used for the prefetch after the last block.
 constexpr int kOutOfRange = 0x7FFFFFF0;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 struct Rows {  // element strides of a (B, H, N, 64) operand (last dim dense)
   long long b, h, n;
@@ -100,81 +109,120 @@ __device__ __forceinline__ float quad_sum(float x) {
   return x;
 }
 
-// This lane's share of one 32-key block: keys key0 and key0 + 16 (r = 0, 1), each as two
+// This lane's share of one block of a wave: keys key0 + 16r (r < kKeysPerLane), each as two
 // 16-byte pieces: dims 8c .. 8c+7 (piece 0, bytes 16c) and 32+8c .. +7 (piece 1, bytes
 // 64+16c).  A wave instruction reads 16 rows x 64 contiguous bytes.
 struct KV {
-  u32x4 k[2][2], v[2][2];
+  u32x4 k[kKeysPerLane][2], v[kKeysPerLane][2];
 };
 
-// kb: the block's first key (wave-uniform); k_lane/v_lane: this lane's byte offsets within a
-// block, (l/4 + 16r) * row + 16c.  A block that is not live loads from kOutOfRange (+ the
+// kb: the block's first key (wave-uniform); k_lane/v_lane: this lane's byte offset within a
+// block, (l/4) * row + 16c; key r of the lane is 16r rows further.  A block that is not live loads from kOutOfRange (+ the
 // lane part, still past num_records as an unsigned 32-bit offset).
 __device__ __forceinline__ void load_block(KV& x, __amdgpu_buffer_rsrc_t kd,
                                            __amdgpu_buffer_rsrc_t vd, int krow, int vrow, int kb,
-                                           bool live, const int (&k_lane)[2],
-                                           const int (&v_lane)[2]) {
+                                           bool live, int k_lane, int v_lane) {
   const int ks = __builtin_amdgcn_readfirstlane(live ? kb * krow : kOutOfRange);
   const int vs = __builtin_amdgcn_readfirstlane(live ? kb * vrow : kOutOfRange);
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int r = 0; r < kKeysPerLane; ++r)
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      x.k[r][p] = load16(kd, ks + k_lane[r] + 64 * p);
-      x.v[r][p] = load16(vd, vs + v_lane[r] + 64 * p);
+      x.k[r][p] = load16(kd, ks + k_lane + 16 * r * krow + 64 * p);
+      x.v[r][p] = load16(vd, vs + v_lane + 16 * r * vrow + 64 * p);
     }
 }
 
-// Online-softmax update of this key column's stream (m, l, o[16]) with the block's 2 keys.
-__device__ __forceinline__ void block_update(const KV& x, const float (&qf)[16], int key0,
-                                             int key_end, float& m, float& l, float (&o)[16]) {
-  float s[2];
+// bf16 pair helpers: v_dot2_f32_bf16 (a.lo*b.lo + a.hi*b.hi + c, fp32 accumulate; products
+// of bf16 values are exact in fp32) and v_perm_b32 byte selection.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                         __builtin_bit_cast(bf16x2, b), c, false);
+}
+// (x.lo16, y.lo16) and (x.hi16, y.hi16): one head dim of two keys side by side.
+__device__ __forceinline__ uint32_t pair_lo(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pair_hi(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+// Online-softmax update of this key column's stream (m, l, o[16]) with the lane's keys of
+// the block.
+//   scores: q . k as bf16 dot2 (q kept in bf16, exact products), times scale*log2(e);
+//   o += p_r v_r + p_r+1 v_r+1 as bf16 dot2 of (p_r, p_r+1) with (v_r[d], v_r+1[d]) built by
+//   v_perm; p is rounded to bf16 for that product (as the forward kernel's P operand), l sums
+//   it in fp32.
+//   The running max is exact, so the largest weight of the stream is exactly 1.
+//   o and l are rescaled only when some lane's max moved (wave-uniform test).
+__device__ __forceinline__ void block_update(const KV& x, const uint32_t (&qp)[8],
+                                             float scale_log2, int key0, int key_end, float& m,
+                                             float& l, float (&o)[16]) {
+  float s[kKeysPerLane];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
+  for (int r = 0; r < kKeysPerLane; ++r) {
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      acc0 = fmaf(qf[2 * i], bf_lo(x.k[r][0][i]), acc0);
-      acc0 = fmaf(qf[2 * i + 1], bf_hi(x.k[r][0][i]), acc0);
-      acc1 = fmaf(qf[8 + 2 * i], bf_lo(x.k[r][1][i]), acc1);
-      acc1 = fmaf(qf[8 + 2 * i + 1], bf_hi(x.k[r][1][i]), acc1);
+      acc0 = dot2(qp[i], x.k[r][0][i], acc0);
+      acc1 = dot2(qp[4 + i], x.k[r][1][i], acc1);
     }
-    const float acc = quad_sum(acc0 + acc1);
+    const float acc = quad_sum(acc0 + acc1) * scale_log2;
     s[r] = (key0 + 16 * r < key_end) ? acc : -INFINITY;
   }
-  const float m_new = fmaxf(m, fmaxf(s[0], s[1]));
+  float m_new = m;
+#pragma unroll
+  for (int r = 0; r < kKeysPerLane; ++r) m_new = fmaxf(m_new, s[r]);
+  const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+  if (__builtin_amdgcn_ballot_w64(m_new != m)) {
+    const float alpha = exp2f(m - m_use);
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] *= alpha;
+  }
+#pragma unroll
+  for (int r = 0; r < kKeysPerLane; r += 2) {
+    const float p0 = exp2f(s[r] - m_use), p1 = exp2f(s[r + 1] - m_use);
+    l += p0 + p1;
+    const bf16x2 pb = {(__bf16)p0, (__bf16)p1};
+    const uint32_t pp = __builtin_bit_cast(uint32_t, pb);
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[8 * p + 2 * i] = dot2(pp, pair_lo(x.v[r][p][i], x.v[r + 1][p][i]), o[8 * p + 2 * i]);
+        o[8 * p + 2 * i + 1] =
+            dot2(pp, pair_hi(x.v[r][p][i], x.v[r + 1][p][i]), o[8 * p + 2 * i + 1]);
+      }
+  }
+  m = m_new;
+}
+
+// The new token as one more key of the stream of key column 0 (lanes 0..3) of the calling
+// wave; every other column sees it masked.  kn/vn: this lane's pieces of k_new and v_new.
+__device__ __forceinline__ void new_key_update(const u32x4 (&kn)[2], const u32x4 (&vn)[2],
+                                               const uint32_t (&qp)[8], float scale_log2,
+                                               bool mine, float& m, float& l, float (&o)[16]) {
+  float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc0 = dot2(qp[i], kn[0][i], acc0);
+    acc1 = dot2(qp[4 + i], kn[1][i], acc1);
+  }
+  const float sc = mine ? quad_sum(acc0 + acc1) * scale_log2 : -INFINITY;
+  const float m_new = fmaxf(m, sc);
   const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
   const float alpha = exp2f(m - m_use);
-  const float p0 = exp2f(s[0] - m_use), p1 = exp2f(s[1] - m_use);
-  l = fmaf(l, alpha, p0 + p1);
+  const float pn = exp2f(sc - m_use);
+  l = fmaf(l, alpha, pn);
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float a = o[8 * p + 2 * i] * alpha, b = o[8 * p + 2 * i + 1] * alpha;
-      a = fmaf(p0, bf_lo(x.v[0][p][i]), a);
-      b = fmaf(p0, bf_hi(x.v[0][p][i]), b);
-      a = fmaf(p1, bf_lo(x.v[1][p][i]), a);
-      b = fmaf(p1, bf_hi(x.v[1][p][i]), b);
-      o[8 * p + 2 * i] = a;
-      o[8 * p + 2 * i + 1] = b;
+      o[8 * p + 2 * i] = fmaf(pn, bf_lo(vn[p][i]), o[8 * p + 2 * i] * alpha);
+      o[8 * p + 2 * i + 1] = fmaf(pn, bf_hi(vn[p][i]), o[8 * p + 2 * i + 1] * alpha);
     }
   m = m_new;
-}
-
-// The new token's row replaces the (zero-filled) loads of cache row Lc in the block that
-// holds it.
-__device__ __forceinline__ void put_new(KV& x, int key0, int Lc, const u32x4 (&kn)[2],
-                                        const u32x4 (&vn)[2]) {
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-    if (key0 + 16 * r == Lc) {
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        x.k[r][p] = kn[p];
-        x.v[r][p] = vn[p];
-      }
-    }
 }
 
 __global__ __launch_bounds__(kThreads) void decode_kernel(
@@ -182,8 +230,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     const __bf16* __restrict__ Kn, Vecs kns, const __bf16* __restrict__ Vn, Vecs vns,
     const int* __restrict__ seqlens, __bf16* __restrict__ O, Vecs os, float* __restrict__ LSE,
     float* __restrict__ part, int H, int N_max, int S, int C, float scale_log2) {
-  __shared__ float sh_o[kStreams][kD];
+  constexpr int kStreams = kWaves * kGroups;       // softmax streams of the workgroup
+  constexpr int kParts = kThreads / kD;            // first-level merge: streams in kParts parts
+  constexpr int kPerPart = kStreams / kParts;
+  __shared__ float sh_o[kStreams][kD + 1];         // +1: stream-major writes, dim-major reads
   __shared__ float sh_m[kStreams], sh_l[kStreams];
+  __shared__ float sh_po[kParts][kD], sh_pm[kParts], sh_pl[kParts];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -229,17 +281,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     }
   }
 
-  float qf[16];
+  uint32_t qp[8];  // this lane's q pieces as bf16 pairs (dims 8c.. and 32+8c..)
   {
     const __bf16* qh = Q + b * qs.b + h * qs.h;
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const u32x4 qv = *reinterpret_cast<const u32x4*>(qh + 32 * p + 8 * c);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        qf[8 * p + 2 * i] = bf_lo(qv[i]) * scale_log2;
-        qf[8 * p + 2 * i + 1] = bf_hi(qv[i]) * scale_log2;
-      }
+      for (int i = 0; i < 4; ++i) qp[4 * p + i] = qv[i];
     }
   }
 
@@ -250,32 +299,41 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   // Blocks of this wave: kb = c0 + 32*wave + 128*t.  Two register sets used in turn, so the
   // next block's loads are in flight while the current one is computed, with no copies
   // between the sets (a copy would wait for the loads).
+  // Cached rows of this chunk: [c0, ce).  The appended row (Lc, if it falls in this chunk) is
+  // not read from the cache; wave 0 folds it in after the loop.
+  const int ce = min(c1, Lc);
   int kb = c0 + wave * kWaveKeys;
-  if (kb < c1) {
-    const int nblk = (c1 - kb + kBlockKeys - 1) / kBlockKeys;  // this wave's blocks
-    const int k_lane[2] = {g * krow + 16 * c, (g + 16) * krow + 16 * c};
-    const int v_lane[2] = {g * vrow + 16 * c, (g + 16) * vrow + 16 * c};
+  if (kb < ce) {
+    const int nblk = (ce - kb + kBlockKeys - 1) / kBlockKeys;  // this wave's blocks
+    const int k_lane = g * krow + 16 * c;
+    const int v_lane = g * vrow + 16 * c;
+    // Two register sets used in turn: the next block's loads are in flight while one block
+    // is computed.  Pairs of blocks per iteration, one back edge and no exit inside the body,
+    // so at the top of an iteration only A's loads are outstanding.  (A third set was measured
+    // slower: the compiler then waits for two sets before the first block of an iteration.)
     KV A, B;
     load_block(A, kd, vd, krow, vrow, kb, true, k_lane, v_lane);
-    // Pairs of blocks with one back edge and no exit inside the body: at the top of an
-    // iteration only A's loads are outstanding.
+    // The scheduling barriers keep each block's arithmetic after the loads issued before it:
+    // left alone, the scheduler hoists the (independent) dot products of the next block, which
+    // then wait for the loads just issued.
     for (int t = 0; t + 2 <= nblk; t += 2) {
       load_block(B, kd, vd, krow, vrow, kb + kBlockKeys, true, k_lane, v_lane);
-      if (has_new && Lc >= kb && Lc < kb + kWaveKeys) put_new(A, kb + g, Lc, k_app, v_app);
-      block_update(A, qf, kb + g, c1, m, l, o);
+      __builtin_amdgcn_sched_barrier(0);
+      block_update(A, qp, scale_log2, kb + g, ce, m, l, o);
+      __builtin_amdgcn_sched_barrier(0);
       kb += kBlockKeys;
       load_block(A, kd, vd, krow, vrow, kb + kBlockKeys, t + 2 < nblk, k_lane, v_lane);
-      if (has_new && Lc >= kb && Lc < kb + kWaveKeys) put_new(B, kb + g, Lc, k_app, v_app);
-      block_update(B, qf, kb + g, c1, m, l, o);
+      __builtin_amdgcn_sched_barrier(0);
+      block_update(B, qp, scale_log2, kb + g, ce, m, l, o);
+      __builtin_amdgcn_sched_barrier(0);
       kb += kBlockKeys;
     }
-    if (nblk & 1) {
-      if (has_new && Lc >= kb && Lc < kb + kWaveKeys) put_new(A, kb + g, Lc, k_app, v_app);
-      block_update(A, qf, kb + g, c1, m, l, o);
-    }
+    if (nblk & 1) block_update(A, qp, scale_log2, kb + g, ce, m, l, o);
   }
+  if (has_new && wave == 0) new_key_update(k_app, v_app, qp, scale_log2, g == 0, m, l, o);
 
-  // Merge the 64 streams of the workgroup (16 key columns x 4 waves) in LDS.
+  // Merge the workgroup's 128 streams (16 key columns x 8 waves): every stream to LDS; thread
+  // t folds streams [16*(t/64), +16) for head dim t%64; 64 threads fold the 8 results.
   const int stream = wave * kGroups + g;
 #pragma unroll
   for (int p = 0; p < 2; ++p)
@@ -286,18 +344,39 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     sh_l[stream] = l;
   }
   __syncthreads();
+  {
+    const int d = tid & (kD - 1), part = tid / kD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kPerPart; ++i) M = fmaxf(M, sh_m[part * kPerPart + i]);
+    const float M_use = (M == -INFINITY) ? 0.f : M;
+    float lt = 0.f, ot = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPerPart; ++i) {
+      const int st = part * kPerPart + i;
+      const float w = exp2f(sh_m[st] - M_use);
+      lt = fmaf(w, sh_l[st], lt);
+      ot = fmaf(w, sh_o[st][d], ot);
+    }
+    sh_po[part][d] = ot;
+    if (d == 0) {
+      sh_pm[part] = M;
+      sh_pl[part] = lt;
+    }
+  }
+  __syncthreads();
   if (tid >= kD) return;
   const int d = tid;
   float M = -INFINITY;
-#pragma unroll 8
-  for (int i = 0; i < kStreams; ++i) M = fmaxf(M, sh_m[i]);
+#pragma unroll
+  for (int i = 0; i < kParts; ++i) M = fmaxf(M, sh_pm[i]);
   const float M_use = (M == -INFINITY) ? 0.f : M;
   float lt = 0.f, ot = 0.f;
-#pragma unroll 8
-  for (int i = 0; i < kStreams; ++i) {
-    const float w = exp2f(sh_m[i] - M_use);
-    lt = fmaf(w, sh_l[i], lt);
-    ot = fmaf(w, sh_o[i][d], ot);
+#pragma unroll
+  for (int i = 0; i < kParts; ++i) {
+    const float w = exp2f(sh_pm[i] - M_use);
+    lt = fmaf(w, sh_pl[i], lt);
+    ot = fmaf(w, sh_po[i][d], ot);
   }
   const float on = lt > 0.f ? ot / lt : 0.f;
   const float lse2 = lt > 0.f ? M + log2f(lt) : -INFINITY;
@@ -312,10 +391,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
 }
 
 // Combines the S partials of each head: one wave per head, lane = head dim.
-__global__ __launch_bounds__(kThreads) void decode_merge_kernel(
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float* __restrict__ part, const int* __restrict__ seqlens, __bf16* __restrict__ O,
     Vecs os, float* __restrict__ LSE, int BH, int H, int N_max, int S, bool append) {
-  const int bh = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int bh = blockIdx.x * (kMergeThreads / 64) + (threadIdx.x >> 6);
   if (bh >= BH) return;
   const int d = threadIdx.x & 63;
   const int b = bh / H, h = bh - b * H;
@@ -340,11 +419,13 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(
 // ---------------------------------------------------------------------------------------
 // Host side.
 
-// Splits for a cache of N_max rows: enough workgroups for two per CU, chunks a multiple of
-// kBlockKeys, no empty split.
+// Splits for a cache of N_max rows.  One 8-wave workgroup per head keeps 128 KiB of K/V
+// loads in flight, enough to stream at HBM rate from one CU, so heads are not split while
+// B*H covers at least half the CUs (no partials, no merge kernel); below that, about one
+// workgroup per CU.  Chunks are a multiple of kBlockKeys, no split is empty.
 static void choose_split(int BH, int N_max, int cu_count, int max_splits, int* S_out, int* C_out) {
   const int blocks = std::max(1, (N_max + kBlockKeys - 1) / kBlockKeys);
-  int S = std::max(1, (2 * cu_count + BH - 1) / BH);
+  int S = 2 * BH >= cu_count ? 1 : (cu_count + BH - 1) / BH;
   S = std::min(S, blocks);
   S = std::max(1, std::min(S, max_splits));
   const int C = (blocks + S - 1) / S * kBlockKeys;
@@ -399,7 +480,9 @@ static bool vecs_overlap(const Vecs& v, int B, int H) {
 extern "C" size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max) {
   using namespace tfgfa_decode;
   if (B <= 0 || H <= 0 || N_max <= 0) return 0;
-  const size_t blocks = ((size_t)N_max + kBlockKeys - 1) / kBlockKeys;
+  // One partial per 128 cache rows: an upper bound on the splits of any block size >= 128,
+  // so the size does not change with the kernel's tiling.
+  const size_t blocks = ((size_t)N_max + kWorkspaceRows - 1) / kWorkspaceRows;
   return (size_t)B * (size_t)H * blocks * kPartFloats * sizeof(float);
 }
 
@@ -464,8 +547,9 @@ extern "C" int tfgfa_decode_bf16(const void* q, const int64_t* q_strides, void* 
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return -(int)e;
   if (S > 1) {
-    hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((bh + kWaves - 1) / kWaves)),
-                       dim3(kThreads), 0, stream, static_cast<const float*>(workspace),
+    const int heads_per_wg = kMergeThreads / 64;
+    hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((bh + heads_per_wg - 1) / heads_per_wg)),
+                       dim3(kMergeThreads), 0, stream, static_cast<const float*>(workspace),
                        cache_seqlens, static_cast<__bf16*>(o), os, lse, (int)bh, H, N_max, S,
                        append);
     e = hipGetLastError();
