@@ -2,9 +2,11 @@
 
 Mirrors the reference's model classes (src/py/model_inference.py:39-190) with the same
 names, constructor arguments and config keys, so code written against the reference's
-``GPTModel(cfg)`` runs unchanged.  Only the parts needed to run a forward pass are
-here; the reference's data loader, decoding loop, training helpers and pretrained-weight
-download (model_inference.py:23-37, :193-376; gpt_download.py) are not.
+``GPTModel(cfg)`` runs unchanged, and its token loop ``generate`` (:199-228).  Added:
+``KVCache`` and ``generate_cached``, the same loop with a KV cache (prefill once, then one
+decode-kernel step per token).  The reference's data loader, training helpers, tokenizer and
+pretrained-weight download (model_inference.py:23-37, :193-197, :229-376; gpt_download.py)
+are not here.
 
 ``impl_type`` selects the attention implementation as at model_inference.py:68-90:
   * ``"manual"``     - the reference's explicit PyTorch path (:68-75);
@@ -102,7 +104,9 @@ class MultiHeadAttention(nn.Module):
             "mask", torch.triu(torch.ones(context_length, context_length), diagonal=1)
         )
 
-    def forward(self, x):
+    def forward(self, x, kv_cache=None, layer: int = 0):
+        if kv_cache is not None:
+            return self._forward_cached(x, kv_cache, layer)
         b, num_tokens, _ = x.shape
         queries = self.W_query(x)
         keys = self.W_key(x)
@@ -114,6 +118,69 @@ class MultiHeadAttention(nn.Module):
         context_vec = ATTENTION_IMPLS[self.impl_type](queries, keys, values, mask_bool, self.dropout)
         context_vec = context_vec.contiguous().view(b, num_tokens, self.d_out)
         return self.out_proj(context_vec)
+
+
+    def _forward_cached(self, x, cache, layer):
+        """Attention against a KV cache (no counterpart in the reference, whose generate()
+        re-runs the whole prefix, model_inference.py:199-228).
+
+        Prefill (the cache is empty): the new tokens' K/V are copied into the cache and the
+        causal forward kernel reads Q from the projection and K/V from the cache through their
+        strides.  Decode (one new token): the decode kernel appends the token's K/V to the cache
+        and attends over the cached prefix.  Both write the context straight into a
+        (B, N, H*d) buffer.
+        """
+        import custom_flash_attn  # raises if the native extension is not built
+
+        if self.impl_type not in ("hip", "cuda"):
+            raise ValueError(f"cached attention runs on the HIP kernels; impl_type is {self.impl_type!r}")
+        b, n, _ = x.shape
+        H, hd = self.num_heads, self.head_dim
+        q = self.W_query(x).view(b, n, H, hd)
+        k = self.W_key(x).view(b, n, H, hd)
+        v = self.W_value(x).view(b, n, H, hd)
+        kc, vc = cache.k[layer], cache.v[layer]
+        ctx = torch.empty(b, n, H, hd, dtype=q.dtype, device=q.device)
+        if cache.length == 0:
+            if n > kc.shape[2]:
+                raise ValueError(f"{n} tokens do not fit a cache of {kc.shape[2]}")
+            kc[:, :, :n].copy_(k.transpose(1, 2))
+            vc[:, :, :n].copy_(v.transpose(1, 2))
+            custom_flash_attn.attention(q.transpose(1, 2), kc[:, :, :n], vc[:, :, :n],
+                                        out=ctx.transpose(1, 2))
+        elif n == 1:
+            custom_flash_attn.decode(q[:, 0], kc, vc, cache.seqlens, k[:, 0], v[:, 0],
+                                     out=ctx[:, 0], workspace=cache.workspace)
+        else:
+            raise NotImplementedError("a cache that already holds tokens takes one new token per step")
+        return self.out_proj(ctx.view(b, n, self.d_out))
+
+
+class KVCache:
+    """Per-layer K/V caches of a GPTModel for cached decoding.
+
+    ``k[layer]``, ``v[layer]``: (B, H, max_len, head_dim) bf16 on ``device`` (each head's rows
+    contiguous, which the decode kernel streams); ``seqlens``: int32 (B,) on the device, the
+    cached rows per batch row; ``length``: the same count on the host.  ``workspace`` holds
+    the decode kernel's split partials.
+    """
+
+    def __init__(self, cfg: dict, batch: int, max_len: int, device, dtype=torch.bfloat16):
+        import custom_flash_attn
+
+        H = cfg["n_heads"]
+        hd = cfg["emb_dim"] // H
+        self.max_len = max_len
+        self.k = [torch.zeros(batch, H, max_len, hd, dtype=dtype, device=device) for _ in range(cfg["n_layers"])]
+        self.v = [torch.zeros(batch, H, max_len, hd, dtype=dtype, device=device) for _ in range(cfg["n_layers"])]
+        self.seqlens = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.length = 0
+        nbytes = custom_flash_attn._C.decode_workspace_bytes(batch, H, max_len)
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+    def advance(self, n: int) -> None:
+        self.length += n
+        self.seqlens.add_(n)
 
 
 class LayerNorm(nn.Module):
@@ -169,13 +236,13 @@ class TransformerBlock(nn.Module):
         self.norm2 = LayerNorm(cfg)
         self.drop_shortcut = nn.Dropout(cfg["drop_rate"])
 
-    def forward(self, x):
+    def forward(self, x, kv_cache=None, layer: int = 0):
         shortcut = x
         x = self.norm1(x)
         # model_inference.py:153 - autocast only has an effect for CUDA(HIP) tensors, so it
         # is switched on only for them (same result, no warning on CPU-only hosts).
         with torch.autocast(device_type="cuda", dtype=torch.bfloat16, enabled=x.is_cuda):
-            x = self.att(x)
+            x = self.att(x, kv_cache, layer)
         x = self.drop_shortcut(x)
         x = x + shortcut
         shortcut = x
@@ -197,14 +264,75 @@ class GPTModel(nn.Module):
         self.final_norm = LayerNorm(cfg)
         self.out_head = nn.Linear(cfg["emb_dim"], cfg["vocab_size"], bias=False)
 
-    def forward(self, in_idx):
+    def forward(self, in_idx, kv_cache=None):
+        """Logits for ``in_idx``.  With ``kv_cache`` the tokens continue the cached sequence:
+        positions start at ``kv_cache.length`` and the cache advances by the token count."""
         _, seq_len = in_idx.shape
+        start = 0 if kv_cache is None else kv_cache.length
         tok_embeds = self.tok_emb(in_idx)
-        pos_embeds = self.pos_emb(torch.arange(seq_len, device=in_idx.device))
+        pos_embeds = self.pos_emb(torch.arange(start, start + seq_len, device=in_idx.device))
         x = self.drop_emb(tok_embeds + pos_embeds)
-        x = self.trf_blocks(x)
+        if kv_cache is None:
+            x = self.trf_blocks(x)
+        else:
+            for layer, blk in enumerate(self.trf_blocks):
+                x = blk(x, kv_cache, layer)
+            kv_cache.advance(seq_len)
         x = self.final_norm(x)
         return self.out_head(x)
+
+
+def _next_token(logits, temperature, top_k):
+    # model_inference.py:207-222: optional top-k filter, then temperature sampling or argmax.
+    # The reference takes min_val = top_logits[:, -1], shape (B,), which broadcasts against the
+    # (B, vocab) logits only for B = 1; here it keeps a column, (B, 1), so batches work too.
+    if top_k is not None:
+        top_logits, _ = torch.topk(logits, top_k)
+        min_val = top_logits[:, -1:]
+        logits = torch.where(logits < min_val, torch.tensor(float("-inf"), device=logits.device), logits)
+    if temperature > 0.0:
+        logits = logits / temperature
+        probs = torch.softmax(logits, dim=-1)
+        return torch.multinomial(probs, num_samples=1)
+    return torch.argmax(logits, dim=-1, keepdim=True)
+
+
+def generate(model, idx, max_new_tokens, context_size, temperature=1.0, top_k=None, eos_id=None):
+    """The reference's token loop (model_inference.py:199-228): every step re-runs the model
+    over the last ``context_size`` tokens and samples from the last position's logits."""
+    for _ in range(max_new_tokens):
+        idx_cond = idx[:, -context_size:]
+        with torch.no_grad():
+            logits = model(idx_cond)[:, -1, :]
+        idx_next = _next_token(logits, temperature, top_k)
+        if idx_next == eos_id:
+            break
+        idx = torch.cat((idx, idx_next), dim=1)
+    return idx
+
+
+def generate_cached(model, idx, max_new_tokens, context_size, temperature=1.0, top_k=None,
+                    eos_id=None):
+    """:func:`generate` with a KV cache: one prefill over the prompt, then one decode step per
+    new token (the decode kernel, which appends the token's K/V and attends over the cache).
+    Same sampling.  The whole sequence must fit ``context_size`` (no sliding window: shifting
+    positions would invalidate the cache)."""
+    if idx.shape[1] + max_new_tokens > context_size:
+        raise ValueError(f"prompt ({idx.shape[1]}) + max_new_tokens ({max_new_tokens}) exceeds "
+                         f"context_size ({context_size})")
+    cfg = {"n_heads": model.trf_blocks[0].att.num_heads, "emb_dim": model.tok_emb.embedding_dim,
+           "n_layers": len(model.trf_blocks)}
+    cache = KVCache(cfg, idx.shape[0], idx.shape[1] + max_new_tokens, idx.device)
+    step_in = idx
+    for _ in range(max_new_tokens):
+        with torch.no_grad():
+            logits = model(step_in, kv_cache=cache)[:, -1, :]
+        idx_next = _next_token(logits, temperature, top_k)
+        if idx_next == eos_id:
+            break
+        idx = torch.cat((idx, idx_next), dim=1)
+        step_in = idx_next
+    return idx
 
 
 # Base config (model_inference.py:378-386) and the sizes of model_inference.py:393-397; the
