@@ -184,12 +184,44 @@ def time_decode(dev, steps, warmup):
         step(i)
     end.record(stream)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    ms_eager = start.elapsed_time(end) / steps
+
+    # A decode step is ~13 us of GPU work, close to what one host launch costs, so launches
+    # from Python can leave gaps (a profiler's launch hooks do).  Serving loops replay steps
+    # from a HIP graph: also time DEC_SETS * 4 captured steps (the caches rotate inside the
+    # graph), replayed.
+    per_graph = DEC_SETS * 4
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            sh_cap = torch.cuda.current_stream(dev).cuda_stream
+            for i in range(per_graph):
+                q, kc, vc, kn, vn = sets[i % DEC_SETS]
+                _C.decode(q.data_ptr(), q.stride(), kc.data_ptr(), kc.stride(), vc.data_ptr(),
+                          vc.stride(), kn.data_ptr(), kn.stride(), vn.data_ptr(), vn.stride(),
+                          seqlens.data_ptr(), o.data_ptr(), o.stride(), lse.data_ptr(), B, H, N, D,
+                          SCALE, ws.data_ptr(), ws_bytes, sh_cap)
+    stream.wait_stream(side)
+    replays = max(1, steps // per_graph)
+    for _ in range(max(1, warmup // per_graph)):
+        graph.replay()
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_graph = start.elapsed_time(end) / (replays * per_graph)
+    ms = ms_eager
     gbs = decode_bytes() / (ms * 1e-3) / 1e9
     return {
         "workload": f"decode step, B={B} H={H} d={D}, cache {N} rows ({N - 1} valid + 1 appended), "
                     f"O + LSE, {DEC_SETS} rotating caches",
         "ms_per_step": round(ms, 5), "steps": steps,
+        "ms_per_step_graph": round(ms_graph, 5),
+        "graph": f"{per_graph} captured steps replayed {replays} times",
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                      "algorithmic_bytes": decode_bytes()},
