@@ -40,19 +40,24 @@
 extern "C" {
 #endif
 
-#define TFGFA_ABI_VERSION 3
+#define TFGFA_ABI_VERSION 4
 
 /* Status codes (> 0: invalid argument). */
 #define TFGFA_OK                 0
 #define TFGFA_ERR_NULL_POINTER   1  /* q, k, v or o is NULL                          */
 #define TFGFA_ERR_BAD_SHAPE      2  /* B, H or N negative                            */
-#define TFGFA_ERR_HEAD_DIM       3  /* D is not a compiled head dimension (only 64)  */
+#define TFGFA_ERR_HEAD_DIM       3  /* D not a multiple of 8 in [8, 128] (fwd), not 64 (decode) */
 #define TFGFA_ERR_SCALE          4  /* softmax_scale not finite or not > 0           */
 #define TFGFA_ERR_CAUSAL_FLAG    5  /* causal is neither 0 nor 1                     */
 #define TFGFA_ERR_TOO_LARGE      6  /* grid or element count exceeds the limits      */
 #define TFGFA_ERR_ALIGNMENT      7  /* q/k/v/o not 16-byte aligned or lse not 4-byte */
 #define TFGFA_ERR_STRIDE         8  /* strides outside what the entry point takes         */
 #define TFGFA_ERR_CACHE          9  /* k_new/v_new given without cache_seqlens            */
+#define TFGFA_ERR_DTYPE         10  /* dtype is not a TFGFA_DTYPE_* value                 */
+
+/* Element types of q, k, v, o (fp32 accumulation and softmax either way). */
+#define TFGFA_DTYPE_BF16 0
+#define TFGFA_DTYPE_F16  1
 
 /*
  * Attention forward, bf16 in / bf16 out, fp32 accumulation and softmax.
@@ -63,7 +68,8 @@ extern "C" {
  * Replaces flashattention_forward<__nv_bfloat16>(O, Q, K_mat, V, seq_len,
  * batch_size, num_heads) (src/cpp/v1.cu:4-38, instantiated :40-42), whose
  * scale is fixed to 1/sqrt(64) (v1.cu:16) and whose launch goes to the legacy
- * default stream (v1.cu:33-34).  Here the scale is explicit (pass 0.125 for
+ * default stream (v1.cu:33-34).  D: a multiple of 8 up to 128 (the reference
+ * compiles 64 only, common_types.hpp:33); tfgfa_fwd with dtype bf16, N_q = N_k.  Here the scale is explicit (pass 0.125 for
  * the reference's behaviour), `lse` may be NULL, and `hip_stream` (a
  * hipStream_t, NULL = default stream) is the stream the caller is using.
  * B, H or N equal to 0 is an empty problem: nothing is launched and 0 is returned,
@@ -72,6 +78,25 @@ extern "C" {
 int tfgfa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
                    int B, int H, int N, int D, float softmax_scale, int causal,
                    void* hip_stream);
+
+/*
+ * The general forward: the surface of the reference's Triton wrapper
+ * _flash_attn_forward(q, k, v, softmax_scale) (src/py/triton_implementation.py:184-197,
+ * kernel :15-181): q (B, H, N_q, D), k and v (B, H, N_k, D), o like q, all strided
+ * (4 element strides each, b/h/n/d, NULL = contiguous; rules as for
+ * tfgfa_fwd_bf16_strided below with "n >= D" for "n >= 64"), dtype
+ * TFGFA_DTYPE_BF16 or TFGFA_DTYPE_F16, D any multiple of 8 from 8 to 128
+ * (the Triton wrapper's d <= 128, :190), an explicit scale.  With causal == 1
+ * the mask is top-left aligned as in the Triton kernel (:127): query i sees keys
+ * j <= i and j < N_k.  N_k == 0 with N_q > 0 is TFGFA_ERR_BAD_SHAPE.  LSE, when
+ * requested, is contiguous (B, H, N_q) float32.
+ */
+int tfgfa_fwd(const void* q, const int64_t* q_strides,
+              const void* k, const int64_t* k_strides,
+              const void* v, const int64_t* v_strides,
+              void* o, const int64_t* o_strides, float* lse,
+              int B, int H, int N_q, int N_k, int D, int dtype,
+              float softmax_scale, int causal, void* hip_stream);
 
 /*
  * The same attention over strided operands: each of q, k, v, o is described by

@@ -52,11 +52,12 @@ def sha256_bf16(x: np.ndarray) -> str:
 def attention_np(q, k, v, scale: float | None = None, causal: bool = True):
     """fp64 restatement of the reference's "manual" branch (src/py/model_inference.py:68-75).
 
-    q, k, v: arrays (..., N, D).  Returns (o, lse) in float64 with o of q's shape and
-    lse of shape (..., N): lse_i = log(sum_{j<=i} exp(scale * q_i.k_j)) as
-    src/py/triton_implementation.py:153-154 accumulates it.  The causal mask is
-    triu(ones, diagonal=1) -> -inf (model_inference.py:55, :70-71): key j is visible to
-    query i iff j <= i.
+    q: (..., N_q, D); k, v: (..., N_k, D) (N_k = N_q in the reference's model; the Triton
+    wrapper allows N_k != N_q, src/py/triton_implementation.py:185-189).  Returns (o, lse) in
+    float64 with o of q's shape and lse of shape (..., N_q): lse_i = log(sum_j exp(scale *
+    q_i.k_j)) as src/py/triton_implementation.py:153-154 accumulates it.  The causal mask is
+    triu(ones, diagonal=1) -> -inf (model_inference.py:55, :70-71), top-left aligned for
+    N_q != N_k as in the Triton kernel (:127): key j is visible to query i iff j <= i.
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)

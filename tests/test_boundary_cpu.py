@@ -42,6 +42,9 @@ def lib():
         ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.tfgfa_decode_workspace_bytes.restype = ctypes.c_size_t
     lib.tfgfa_decode_workspace_bytes.argtypes = [ctypes.c_int] * 3
+    lib.tfgfa_fwd.restype = ctypes.c_int
+    lib.tfgfa_fwd.argtypes = [ctypes.c_void_p, ctypes.c_void_p] * 4 + [ctypes.c_void_p] + [
+        ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
     lib.tfgfa_strerror.restype = ctypes.c_char_p
     lib.tfgfa_strerror.argtypes = [ctypes.c_int]
     lib.tfgfa_abi_version.restype = ctypes.c_int
@@ -51,7 +54,7 @@ def lib():
 def test_library_exports_every_declared_symbol(lib):
     names = _header_functions()
     assert names == ["tfgfa_abi_version", "tfgfa_decode_bf16", "tfgfa_decode_workspace_bytes",
-                     "tfgfa_device_info", "tfgfa_fwd_bf16", "tfgfa_fwd_bf16_strided",
+                     "tfgfa_device_info", "tfgfa_fwd", "tfgfa_fwd_bf16", "tfgfa_fwd_bf16_strided",
                      "tfgfa_strerror"]
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/tfgfa.h but not exported"
@@ -66,7 +69,7 @@ def test_strerror_covers_every_status(lib):
     codes = [_header_define(n) for n in (
         "TFGFA_OK", "TFGFA_ERR_NULL_POINTER", "TFGFA_ERR_BAD_SHAPE", "TFGFA_ERR_HEAD_DIM",
         "TFGFA_ERR_SCALE", "TFGFA_ERR_CAUSAL_FLAG", "TFGFA_ERR_TOO_LARGE", "TFGFA_ERR_ALIGNMENT",
-        "TFGFA_ERR_STRIDE", "TFGFA_ERR_CACHE")]
+        "TFGFA_ERR_STRIDE", "TFGFA_ERR_CACHE", "TFGFA_ERR_DTYPE")]
     msgs = [lib.tfgfa_strerror(c).decode() for c in codes]
     assert len(set(msgs)) == len(msgs)
     assert lib.tfgfa_strerror(12345).decode() == "unknown tfgfa status"
@@ -82,8 +85,9 @@ P = 0x10000
     ((P, P, P, 0, 0, 1, 1, 16, 64, 0.125, 1), "TFGFA_ERR_NULL_POINTER"),
     ((P, P, P, P, 0, -1, 1, 16, 64, 0.125, 1), "TFGFA_ERR_BAD_SHAPE"),
     ((P, P, P, P, 0, 1, 1, -16, 64, 0.125, 1), "TFGFA_ERR_BAD_SHAPE"),
-    ((P, P, P, P, 0, 1, 1, 16, 128, 0.125, 1), "TFGFA_ERR_HEAD_DIM"),
-    ((P, P, P, P, 0, 1, 1, 16, 32, 0.125, 1), "TFGFA_ERR_HEAD_DIM"),
+    ((P, P, P, P, 0, 1, 1, 16, 136, 0.125, 1), "TFGFA_ERR_HEAD_DIM"),   # > 128
+    ((P, P, P, P, 0, 1, 1, 16, 36, 0.125, 1), "TFGFA_ERR_HEAD_DIM"),    # not a multiple of 8
+    ((P, P, P, P, 0, 1, 1, 16, 0, 0.125, 1), "TFGFA_ERR_HEAD_DIM"),
     ((P, P, P, P, 0, 1, 1, 16, 64, 0.0, 1), "TFGFA_ERR_SCALE"),
     ((P, P, P, P, 0, 1, 1, 16, 64, -0.125, 1), "TFGFA_ERR_SCALE"),
     ((P, P, P, P, 0, 1, 1, 16, 64, float("nan"), 1), "TFGFA_ERR_SCALE"),
@@ -97,7 +101,9 @@ P = 0x10000
     ((P, P, P, P, 0, 0, 4, 16, 64, 0.125, 1), "TFGFA_OK"),   # empty problem: nothing launched
     ((P, P, P, P, 0, 2, 4, 0, 64, 0.125, 0), "TFGFA_OK"),
     ((0, 0, 0, 0, 0, 2, 4, 0, 64, 0.125, 1), "TFGFA_OK"),     # empty tensors have NULL data
-    ((0, 0, 0, 0, 0, 2, 4, 0, 128, 0.125, 1), "TFGFA_ERR_HEAD_DIM"),  # sizes checked first
+    ((0, 0, 0, 0, 0, 2, 4, 0, 132, 0.125, 1), "TFGFA_ERR_HEAD_DIM"),  # sizes checked first
+    ((0, P, P, P, 0, 1, 1, 16, 128, 0.125, 1), "TFGFA_ERR_NULL_POINTER"),  # d = 128 accepted
+    ((0, P, P, P, 0, 1, 1, 16, 8, 0.125, 1), "TFGFA_ERR_NULL_POINTER"),    # d = 8 accepted
 ])
 def test_c_abi_argument_validation(lib, args, code):
     assert lib.tfgfa_fwd_bf16(*args, None) == _header_define(code)
@@ -165,7 +171,7 @@ def test_c_abi_strided_output_overlap(lib, os_, code):
 def test_c_abi_strided_checks_sizes_before_strides(lib):
     bad = _st(0, 0, 1, 5)
     assert lib.tfgfa_fwd_bf16_strided(None, bad, None, bad, None, bad, None, bad, None,
-                                      1, 1, 16, 128, 0.125, 1, None) == _header_define("TFGFA_ERR_HEAD_DIM")
+                                      1, 1, 16, 132, 0.125, 1, None) == _header_define("TFGFA_ERR_HEAD_DIM")
     ok = _contig(1, 1, 16)
     assert lib.tfgfa_fwd_bf16_strided(P + 2, ok, P, ok, P, ok, P, ok, None,
                                       1, 1, 16, 64, 0.125, 1, None) == _header_define("TFGFA_ERR_ALIGNMENT")
@@ -248,9 +254,46 @@ def test_pybind_decode_raises_runtime_error_with_message():
                   2, 3, 100, 32, 0.125, 0, 0, 0)
 
 
+def _fwd_args(q=None, k=None, v=None, o=None, lse=None, qs=None, ks=None, vs=None, os_=None, B=2,
+              H=3, Nq=50, Nk=70, D=96, dtype=0, scale=0.125, causal=1):
+    return (q, qs, k, ks, v, vs, o, os_, lse, B, H, Nq, Nk, D, dtype, scale, causal, None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(), "TFGFA_ERR_NULL_POINTER"),                      # N_q != N_k, D = 96, NULL strides
+    (dict(dtype=1, D=128), "TFGFA_ERR_NULL_POINTER"),        # fp16
+    (dict(dtype=2), "TFGFA_ERR_DTYPE"),
+    (dict(dtype=-1), "TFGFA_ERR_DTYPE"),
+    (dict(D=100), "TFGFA_ERR_HEAD_DIM"),
+    (dict(D=144), "TFGFA_ERR_HEAD_DIM"),
+    (dict(Nk=0), "TFGFA_ERR_BAD_SHAPE"),                     # queries but no keys
+    (dict(Nq=0, Nk=0), "TFGFA_OK"),                          # empty
+    (dict(Nq=-1), "TFGFA_ERR_BAD_SHAPE"),
+    (dict(ks=(70 * 3 * 96, 96, 3 * 96, 1)), "TFGFA_ERR_NULL_POINTER"),   # (B, N_k, H, D) view
+    (dict(ks=(70 * 3 * 96, 96, 64, 1)), "TFGFA_ERR_STRIDE"),             # row stride < D
+    (dict(qs=(50 * 3 * 104, 50 * 104, 104, 1)), "TFGFA_ERR_NULL_POINTER"),  # padded rows
+    (dict(os_=(50 * 3 * 96, 96, 96, 1)), "TFGFA_ERR_STRIDE"),            # O heads and rows collide
+    (dict(q=P, k=P, v=P, o=P + 8), "TFGFA_ERR_ALIGNMENT"),
+])
+def test_c_abi_general_forward_validation(lib, kw, code):
+    args = list(_fwd_args(**{k_: v_ for k_, v_ in kw.items() if k_ not in ("qs", "ks", "vs", "os_")}))
+    for key, idx in (("qs", 1), ("ks", 3), ("vs", 5), ("os_", 7)):
+        if key in kw:
+            args[idx] = _st(*kw[key])
+    assert lib.tfgfa_fwd(*args) == _header_define(code)
+
+
+def test_header_dtype_codes():
+    assert _header_define("TFGFA_DTYPE_BF16") == _C.DTYPE_BF16 == 0
+    assert _header_define("TFGFA_DTYPE_F16") == _C.DTYPE_F16 == 1
+
+
 def test_pybind_raises_runtime_error_with_message():
     with pytest.raises(RuntimeError, match="unsupported head dimension"):
-        _C.fwd(P, P, P, P, 0, 1, 1, 16, 128, 0.125, True, 0)
+        _C.fwd(P, P, P, P, 0, 1, 1, 16, 136, 0.125, True, 0)
+    with pytest.raises(RuntimeError, match="tfgfa_fwd failed .*dtype"):
+        _C.fwd_general(P, (0, 0, 64, 1), P, (0, 0, 64, 1), P, (0, 0, 64, 1), P, (0, 0, 64, 1), 0,
+                       1, 1, 16, 16, 64, 5, 0.125, True, 0)
     with pytest.raises(RuntimeError, match="null tensor pointer"):
         _C.fwd(0, P, P, P, 0, 1, 1, 16, 64, 0.125, True, 0)
 
@@ -307,11 +350,13 @@ def test_shim_validation_messages(qkv, msg):
 
 
 @pytest.mark.parametrize("qkv,out,msg", [
-    ((_FakeCuda(dtype=torch.float16), _FakeCuda(), _FakeCuda()), None, r"^Unsupported tensor dtype"),
+    ((_FakeCuda(dtype=torch.float32), _FakeCuda(), _FakeCuda()), None, r"^Unsupported tensor dtype"),
+    ((_FakeCuda(), _FakeCuda(dtype=torch.float16), _FakeCuda()), None, "k must have dtype"),
     ((_FakeCuda(shape=(2, 8, 64)),) * 3, None, "q must be 4-D"),
-    ((_FakeCuda(), _FakeCuda(shape=(1, 2, 9, 64)), _FakeCuda()), None, "k must have shape"),
+    ((_FakeCuda(), _FakeCuda(shape=(1, 3, 9, 64)), _FakeCuda()), None, "k must have shape"),
+    ((_FakeCuda(), _FakeCuda(shape=(1, 2, 9, 64)), _FakeCuda()), None, "v must have shape"),
     ((_FakeCuda(), _FakeCuda(), _FakeCuda(device="cuda:1")), None, "v must be on"),
-    ((_FakeCuda(shape=(1, 2, 8, 128)),) * 3, None, "head_dim must be 64"),
+    ((_FakeCuda(shape=(1, 2, 8, 136)),) * 3, None, r"head_dim must be in \[1, 128\]"),
     ((_FakeCuda(), _FakeCuda(last_stride=2), _FakeCuda()), None, r"k must be dense in its last dimension"),
     ((_FakeCuda(),) * 3, _FakeCuda(shape=(1, 2, 8, 32)), "out must have shape"),
     ((_FakeCuda(),) * 3, _FakeCuda(dtype=torch.float32), r"^Unsupported tensor dtype"),
@@ -321,15 +366,27 @@ def test_attention_view_validation_messages(qkv, out, msg):
     with pytest.raises(RuntimeError, match=msg):
         custom_flash_attn._check_view(qkv[0], "q", None)
         custom_flash_attn._check_view(qkv[1], "k", qkv[0])
-        custom_flash_attn._check_view(qkv[2], "v", qkv[0])
+        custom_flash_attn._check_view(qkv[2], "v", qkv[0], rows_from=qkv[1])
         if out is not None:
-            custom_flash_attn._check_view(out, "out", qkv[0])
+            custom_flash_attn._check_view(out, "out", qkv[0], rows_from=qkv[0])
 
 
 def test_attention_rejects_cpu_tensors():
     q = torch.zeros(1, 1, 4, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="^q must be a CUDA tensor$"):
         custom_flash_attn.attention(q, q, q)
+
+
+@pytest.mark.parametrize("shapes,dtypes,msg", [
+    (((1, 2, 8, 160),) * 3, (torch.bfloat16,) * 3, "head dimensions up to 128"),
+    (((1, 2, 8, 64),) * 3, (torch.bfloat16, torch.float16, torch.bfloat16), "same type"),
+    (((1, 2, 8, 64),) * 3, (torch.float32,) * 3, "fp16 and bf16"),
+    (((1, 2, 8, 64), (1, 2, 9, 64), (1, 2, 10, 64)), (torch.bfloat16,) * 3, None),
+])
+def test_flash_attn_forward_asserts_like_the_triton_wrapper(shapes, dtypes, msg):
+    q, k, v = (torch.zeros(s, dtype=d) for s, d in zip(shapes, dtypes))
+    with pytest.raises(AssertionError, match=msg):
+        custom_flash_attn.flash_attn_forward(q, k, v)
 
 
 def test_forward_is_positional_only():

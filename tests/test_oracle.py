@@ -296,3 +296,24 @@ def test_decode_oracle_empty_and_off_by_one():
     o1, l1 = decode_np(q, kc, vc, [1, 1], 0.125)
     np.testing.assert_allclose(o1, vc[:, :, 0], rtol=0, atol=1e-15)
     np.testing.assert_allclose(l1, 0.125 * np.einsum("bhd,bhd->bh", q.astype(np.float64), kc[:, :, 0].astype(np.float64)), rtol=0, atol=1e-12)
+
+
+# ------------------------------------------------------------------ general forward surface
+
+
+@pytest.mark.parametrize("nq,nk", [(37, 61), (61, 37), (1, 20), (20, 1)])
+@pytest.mark.parametrize("d", [8, 40, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_oracle_nonsquare_and_head_dims_match_sdpa(nq, nk, d, causal):
+    """N_q != N_k with the top-left causal mask of the Triton kernel
+    (triton_implementation.py:127), which torch's SDPA also uses for is_causal with L != S."""
+    q = _rand((2, 3, nq, d), 400 + nq + d, 2.0)
+    k = _rand((2, 3, nk, d), 401 + nk + d, 2.0)
+    v = _rand((2, 3, nk, d), 402 + nk + d)
+    scale = 1.0 / math.sqrt(d)
+    o, lse = attention_np(q, k, v, scale, causal)
+    np.testing.assert_allclose(o, _sdpa64(q, k, v, scale, causal), rtol=0, atol=1e-12)
+    s = np.einsum("bhid,bhjd->bhij", q.astype(np.float64), k.astype(np.float64)) * scale
+    if causal:
+        s = np.where(np.arange(nk)[None, :] > np.arange(nq)[:, None], -np.inf, s)
+    np.testing.assert_allclose(lse, np.log(np.exp(s).sum(-1)), rtol=0, atol=1e-10)

@@ -66,6 +66,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "tfgfa.h"
 
@@ -73,21 +74,25 @@ namespace tfgfa {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kD = 64;                      // head dimension (the only compiled one)
+constexpr int kDHalf = 64;                  // head dims per LDS tile layout ("dim half")
 constexpr int kWaves = 4;                   // waves per workgroup
 constexpr int kThreads = kWaves * 64;       // 256
 constexpr int kWaveRows = 32;               // query rows per wave (one MFMA column block)
 constexpr int kBlockRows = kWaves * kWaveRows;  // 128 query rows per workgroup
 constexpr int kTileKeys = 64;               // keys per K/V tile
-constexpr int kKRowBytes = kD * 2;          // 128 B per K or V row
-constexpr int kHalfTileBytes = kTileKeys * kKRowBytes;  // 8 KiB (K or V)
-constexpr int kTileBytes = 2 * kHalfTileBytes;          // 16 KiB per stage
+constexpr int kKRowBytes = kDHalf * 2;      // 128 B per key row of one dim half in LDS
+constexpr int kHalfTileBytes = kTileKeys * kKRowBytes;  // 8 KiB (K or V, one dim half)
 constexpr int kStages = 3;
-constexpr int kLoadsPerWave = 2 * (kHalfTileBytes / 1024) / kWaves;  // 1 KiB per load instr: 4
+constexpr int kMaxD = 128;
+// A buffer offset past any num_records built here (those stay below 2^31 - 2^24): the load
+// returns zero without a memory access.  Used for head dims past D when D < the tile's dims.
+constexpr int kOutOfRange = 0x7FFFFFF0;
 
 // The exp2 offset is the exact running max of each row (moved whenever a half's max exceeds
 // it).  The row's largest score then gets probability exp2(0) = 1, which bf16 represents
@@ -99,9 +104,26 @@ constexpr float kRescaleThreshold = 0.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
-__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
+// Element type traits: the 16-bit type of Q, K, V, O and of the P operand, its 8-vector, and the
+// matching 32x32x16 MFMA (fp32 accumulate).
+template <typename T>
+struct Elem;
+template <>
+struct Elem<__bf16> {
+  typedef bf16x8 v8;
+  typedef bf16x4 v4;
+  static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Elem<_Float16> {
+  typedef f16x8 v8;
+  typedef f16x4 v4;
+  static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
 
 // Row reductions across the two lane halves (lane l and l^32 hold the same query row).
 // v_permlane32_swap(x, y) exchanges the upper half of x with the lower half of y, so with
@@ -120,16 +142,17 @@ __device__ __forceinline__ float pair_sum(float x) {
 __device__ __forceinline__ int swz_k(int row) { return (row ^ ((row >> 3) & 3)) & 7; }
 __device__ __forceinline__ int swz_v(int row) { return (row & 3) << 1; }
 
-// Buffer descriptor over one head's N rows of 64 bf16 (row r at byte r * row_bytes; row_bytes =
-// 128 for a contiguous head), as four SGPRs for the loads issued from inline assembly: base
-// address, stride 0, num_records = N * row_bytes, format word 0x20000
-// (the layout __builtin_amdgcn_make_buffer_rsrc builds for the Q loads).  A raw buffer load whose
-// byte offset is at or past num_records returns zero: that is the zero-fill of tiles and query
-// blocks past the sequence end (row N starts exactly at num_records; row_bytes >= 128).  The whole offset is kept in the VGPR operand so the range
-// check covers all of it.
+// Buffer descriptor over one head's N rows (row r at byte r * row_bytes; row_bytes = 2 * D for
+// a contiguous head), as four SGPRs for the loads issued from inline assembly: base address,
+// stride 0, num_records = N * row_bytes, format word 0x20000 (the layout
+// __builtin_amdgcn_make_buffer_rsrc builds for the Q loads).  A raw buffer load whose byte
+// offset is at or past num_records returns zero: that is the zero-fill of tiles and query
+// blocks past the sequence end (row N starts exactly at num_records: rows are at least 2D
+// bytes apart and a lane never reads past byte 2D of a row).  The whole offset is kept in the
+// VGPR operand so the range check covers all of it.
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ i32x4 head_desc(const __bf16* base, int N, int row_bytes) {
+__device__ __forceinline__ i32x4 head_desc(const void* base, int N, int row_bytes) {
   const uint64_t b = reinterpret_cast<uint64_t>(base);
   i32x4 d;
   d[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)b);
@@ -157,23 +180,41 @@ __device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
   return (uint32_t)(uintptr_t)(const lds_void*)p;
 }
 
-// This wave's share of one K (or V) tile: rows [8*(2w), 8*(2w+2)) as two 1-KiB LDS blocks.
-// Lane i of a block fills physical chunk i%8 of row i/8, so it fetches the logical chunk that
-// the swizzle maps there.
-template <bool kIsV>
+// Compile-time shape of one kernel instance: head dims kD (64 or 128, = kDH dim halves of 64),
+// element type T, and kMaskD: the actual head dim D may be below kD (a multiple of 8); 16-B
+// chunks of dims >= D load zeros and are not stored.
+template <int kD_, typename T_, bool kMaskD_>
+struct Shape {
+  static constexpr int kD = kD_;
+  static constexpr int kDH = kD_ / kDHalf;
+  static constexpr bool kMaskD = kMaskD_;
+  typedef T_ T;
+  static constexpr int kLoadsPerWave = 4 * kDH;  // transfers per tile step per wave (K and V)
+  static_assert(kD_ == 64 || kD_ == 128, "compiled head dims");
+};
+
+// This wave's share of one K (or V) tile: rows [8*(2w), 8*(2w+2)) of each dim half as two
+// 1-KiB LDS blocks per dim half (dim half dh at byte dh * 8 KiB of the slot).  Lane i of a block
+// fills physical chunk i%8 of row i/8, so it fetches the logical chunk that the swizzle maps
+// there: head dims 64*dh + 8*chunk .. +7, i.e. row bytes 128*dh + 16*chunk.
+template <class Sh, bool kIsV>
 __device__ __forceinline__ void issue_half(i32x4 desc, int row_bytes, unsigned char* dst, int k0,
-                                           int wave, int lane) {
+                                           int wave, int lane, int d_chunks) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int blk = 2 * wave + i;
-    const int row = blk * 8 + (lane >> 3);
-    const int pc = lane & 7;
-    const int sw = kIsV ? swz_v(row) : swz_k(row);
-    // Uniform part (first row of the block) in a scalar register, per-lane part in a vector one.
-    const int s_off = __builtin_amdgcn_readfirstlane((k0 + blk * 8) * row_bytes);
-    lds_transfer(desc, lds_addr(dst + blk * 1024),
-                 s_off + ((lane >> 3) * row_bytes + ((pc ^ sw) << 4)));
-  }
+  for (int dh = 0; dh < Sh::kDH; ++dh)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int blk = 2 * wave + i;
+      const int row = blk * 8 + (lane >> 3);
+      const int pc = lane & 7;
+      const int sw = kIsV ? swz_v(row) : swz_k(row);
+      const int chunk = 8 * dh + (pc ^ sw);  // 16-B chunk of the row in memory
+      // Uniform part (first row of the block) in a scalar register, per-lane part in a vector one.
+      const int s_off = __builtin_amdgcn_readfirstlane((k0 + blk * 8) * row_bytes);
+      int off = s_off + ((lane >> 3) * row_bytes + (chunk << 4));
+      if (Sh::kMaskD) off = chunk < d_chunks ? off : kOutOfRange;
+      lds_transfer(desc, lds_addr(dst + dh * kHalfTileBytes + blk * 1024), off);
+    }
 }
 
 // Workgroup barrier that is also a compiler memory barrier: no LDS access moves across it (the
@@ -189,69 +230,74 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// LDS: a ring of 3 K tiles and a ring of 3 V tiles, each slot its own __shared__ array.  The
-// compiler tracks the buffer_load ... lds transfers and waits for every one of them before an
-// LDS read it cannot prove disjoint; with one array per slot, a transfer into one slot does
-// not hold up reads of another, so the explicit per-step waits are the only ones.
+// LDS: a ring of 3 K tiles and a ring of 3 V tiles, each slot its own __shared__ array of kDH
+// dim halves.
 struct Lds {
   unsigned char* k[kStages];
   unsigned char* v[kStages];
 };
 
 // Per-wave state carried across half-steps.
+template <class Sh>
 struct WaveState {
-  bf16x8 qop[4];   // Q^T operand: Q[qrow][16c + 8h .. +7]
-  f32x16 o0, o1;   // O^T accumulators: d = 0..31 and d = 32..63
-  f32x16 s;        // S^T of the half being softmaxed: register t = key 8(t/4) + 4h + t%4
-  bf16x8 pb[2];    // P^T (bf16) of the previous half, waiting for its P.V
-  float m_run;     // exp2 offset (running max of scale*log2e*s, moved lazily)
-  float l_run;     // running sum of exp2(scale*log2e*s - m_run)
-  int koff[4];     // K A-operand LDS offsets (within a K slot, key half 0)
-  int voff[2][2];  // V^T transposing-read LDS offsets (within a V slot, keys 0..15)
+  typedef typename Elem<typename Sh::T>::v8 v8;
+  v8 qop[4 * Sh::kDH];   // Q^T operand: Q[qrow][16c + 8h .. +7]
+  f32x16 o[2 * Sh::kDH]; // O^T accumulators: o[t] holds d = 32t .. 32t+31
+  f32x16 s;              // S^T of the half being softmaxed: register t = key 8(t/4) + 4h + t%4
+  v8 pb[2];              // P^T of the previous half, waiting for its P.V
+  float m_run;           // exp2 offset (running max of scale*log2e*s)
+  float l_run;           // running sum of exp2(scale*log2e*s - m_run)
+  int koff[4];           // K A-operand LDS offsets (within a K dim half, key half 0)
+  int voff[2][2];        // V^T transposing-read LDS offsets (within a V dim half, keys 0..15)
 };
 
-// S^T = K Q^T for key half kHalf of the tile in K slot kSlot (4 MFMAs).
-template <int kSlot, int kHalf>
-__device__ __forceinline__ f32x16 qk_half(const WaveState& w, const Lds& lds) {
-  const unsigned char* kt = lds.k[kSlot] + kHalf * 32 * kKRowBytes;
+// S^T = K Q^T for key half kHalf of the tile in K slot kSlot (4 MFMAs per dim half).
+template <class Sh, int kSlot, int kHalf>
+__device__ __forceinline__ f32x16 qk_half(const WaveState<Sh>& w, const Lds& lds) {
+  typedef typename Elem<typename Sh::T>::v8 v8;
   f32x16 acc;
 #pragma unroll
   for (int t = 0; t < 16; ++t) acc[t] = 0.f;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(kt + w.koff[c]);
-    acc = mfma32(a, w.qop[c], acc);
+  for (int dh = 0; dh < Sh::kDH; ++dh) {
+    const unsigned char* kt = lds.k[kSlot] + dh * kHalfTileBytes + kHalf * 32 * kKRowBytes;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const v8 a = *reinterpret_cast<const v8*>(kt + w.koff[c]);
+      acc = Elem<typename Sh::T>::mfma(a, w.qop[4 * dh + c], acc);
+    }
   }
   return acc;
 }
 
-// O^T += V^T P^T for key half kHalf of the tile in V slot kSlot, with P^T = w.pb (4 MFMAs).
-// Element e of chunk cc in lane half h is key 16*cc + 8*(e/4) + 4*h + e%4 of the key half:
-// two transposing reads of 4 keys each.
-template <int kSlot, int kHalf>
-__device__ __forceinline__ void pv_half(WaveState& w, const Lds& lds) {
-  const unsigned char* vt = lds.v[kSlot] + kHalf * 32 * kKRowBytes;
+// O^T += V^T P^T for key half kHalf of the tile in V slot kSlot, with P^T = w.pb (4 MFMAs per
+// dim half).  Element e of chunk cc in lane half h is key 16*cc + 8*(e/4) + 4*h + e%4 of the
+// key half: two transposing reads of 4 keys each.
+template <class Sh, int kSlot, int kHalf>
+__device__ __forceinline__ void pv_half(WaveState<Sh>& w, const Lds& lds) {
+  typedef typename Elem<typename Sh::T>::v8 v8;
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc) {
+  for (int dh = 0; dh < Sh::kDH; ++dh) {
+    const unsigned char* vt = lds.v[kSlot] + dh * kHalfTileBytes + kHalf * 32 * kKRowBytes;
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(vt + w.voff[dt][0] + cc * 16 * kKRowBytes));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(vt + w.voff[dt][1] + cc * 16 * kKRowBytes));
-      const bf16x8 va =
-          __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      if (dt == 0)
-        w.o0 = mfma32(va, w.pb[cc], w.o0);
-      else
-        w.o1 = mfma32(va, w.pb[cc], w.o1);
+    for (int cc = 0; cc < 2; ++cc) {
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vt + w.voff[dt][0] + cc * 16 * kKRowBytes));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vt + w.voff[dt][1] + cc * 16 * kKRowBytes));
+        const v8 va = __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        w.o[2 * dh + dt] = Elem<typename Sh::T>::mfma(va, w.pb[cc], w.o[2 * dh + dt]);
+      }
     }
   }
 }
 
 // Masks w.s past the last visible key; lim is the lane's last visible key relative to the
 // half's first key + 4h.
-__device__ __forceinline__ void mask_half(WaveState& w, int lim) {
+template <class Sh>
+__device__ __forceinline__ void mask_half(WaveState<Sh>& w, int lim) {
 #pragma unroll
   for (int t = 0; t < 16; ++t) {
     const int kk = 8 * (t >> 2) + (t & 3);
@@ -260,7 +306,8 @@ __device__ __forceinline__ void mask_half(WaveState& w, int lim) {
 }
 
 // Row max of w.s over the lane pair, scaled to the exp2 domain.
-__device__ __forceinline__ float row_max(const WaveState& w, float scale_log2) {
+template <class Sh>
+__device__ __forceinline__ float row_max(const WaveState<Sh>& w, float scale_log2) {
   float mx = fmaxf(w.s[0], fmaxf(w.s[1], w.s[2]));
 #pragma unroll
   for (int t = 3; t < 15; t += 2) mx = fmaxf(mx, fmaxf(w.s[t], w.s[t + 1]));
@@ -271,7 +318,8 @@ __device__ __forceinline__ float row_max(const WaveState& w, float scale_log2) {
 // Rescale of O and l when some row's max moved (skipped, wave-uniformly, when none did).
 // Every computed half has an unmasked key in every row (it starts at or below the wave's first
 // row), so the max is finite and the first half always moves m_run off -inf.
-__device__ __forceinline__ void rescale(WaveState& w, float m_tile) {
+template <class Sh>
+__device__ __forceinline__ void rescale(WaveState<Sh>& w, float m_tile) {
   const bool grow = m_tile > w.m_run + kRescaleThreshold;
   if (__builtin_amdgcn_ballot_w64(grow) != 0) {
     const float m_new = grow ? m_tile : w.m_run;
@@ -279,16 +327,18 @@ __device__ __forceinline__ void rescale(WaveState& w, float m_tile) {
     w.m_run = m_new;
     w.l_run *= alpha;
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      w.o0[t] *= alpha;
-      w.o1[t] *= alpha;
-    }
+    for (int i = 0; i < 2 * Sh::kDH; ++i)
+#pragma unroll
+      for (int t = 0; t < 16; ++t) w.o[i][t] *= alpha;
   }
 }
 
 // P = exp2(scale*log2e*s - m_run) in fp32, row sum into l (two partial sums), P rounded to
-// bf16 into w.pb: chunk cc (keys 16cc .. 16cc+15 of the half) is registers 8cc .. 8cc+7.
-__device__ __forceinline__ void exp_half(WaveState& w, float scale_log2) {
+// the element type into w.pb: chunk cc (keys 16cc .. 16cc+15 of the half) is registers
+// 8cc .. 8cc+7.
+template <class Sh>
+__device__ __forceinline__ void exp_half(WaveState<Sh>& w, float scale_log2) {
+  typedef typename Sh::T T;
   const float neg_m = -w.m_run;
 #pragma unroll
   for (int t = 0; t < 16; ++t) w.s[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, neg_m));
@@ -301,8 +351,8 @@ __device__ __forceinline__ void exp_half(WaveState& w, float scale_log2) {
   w.l_run += pair_sum(ps0 + ps1);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    w.pb[0][e] = (__bf16)w.s[e];
-    w.pb[1][e] = (__bf16)w.s[8 + e];
+    w.pb[0][e] = (T)w.s[e];
+    w.pb[1][e] = (T)w.s[8 + e];
   }
 }
 
@@ -310,6 +360,7 @@ __device__ __forceinline__ void exp_half(WaveState& w, float scale_log2) {
 struct StepArgs {
   i32x4 k_rsrc, v_rsrc;
   int k_row_bytes, v_row_bytes;  // byte distance between consecutive K (V) rows of a head
+  int d_chunks;  // 16-B chunks of a row holding head dims < D
   int nT;        // 64-key tiles loaded by the workgroup
   int nAct;      // 32-key halves this wave computes (a prefix)
   int nFull;     // halves this wave computes without an element mask (a prefix of the above)
@@ -324,66 +375,78 @@ struct StepArgs {
 //  - u = 0: P is zero and the V slot read was zero-filled, so the P.V adds nothing;
 //  - S_{u+1} is computed even past the wave's last half (finite, discarded).
 // Otherwise (tail): u = nAct is the P.V of the last half only; u > nAct does nothing.
-template <int kVs, int kVh, int kKs, int kKh, bool kSteady>
-__device__ __forceinline__ void half_step(WaveState& w, const Lds& lds, int u,
+template <class Sh, int kVs, int kVh, int kKs, int kKh, bool kSteady>
+__device__ __forceinline__ void half_step(WaveState<Sh>& w, const Lds& lds, int u,
                                           const StepArgs& a) {
   if (!kSteady && u > a.nAct) return;
   if (u >= a.nFull && u < a.nAct) mask_half(w, a.last_key - u * 32 - 4 * a.h);
-  pv_half<kVs, kVh>(w, lds);
+  pv_half<Sh, kVs, kVh>(w, lds);
   const float m_tile = row_max(w, a.scale_log2);
   if (!kSteady && u == a.nAct) return;
   rescale(w, m_tile);
-  const f32x16 n = qk_half<kKs, kKh>(w, lds);
+  const f32x16 n = qk_half<Sh, kKs, kKh>(w, lds);
   exp_half(w, a.scale_log2);
   w.s = n;
 }
 
 // Tile step j (slot kSlot = j % 3): issue K_{j+2}, V_{j+1}; half-step 2j; wait for K_{j+1} and
 // V_j; barrier; half-step 2j+1.
-template <int kSlot, bool kSteady>
-__device__ __forceinline__ void tile_step(WaveState& w, const Lds& lds, int j,
+template <class Sh, int kSlot, bool kSteady>
+__device__ __forceinline__ void tile_step(WaveState<Sh>& w, const Lds& lds, int j,
                                           const StepArgs& a) {
   constexpr int kNext = (kSlot + 1) % kStages;
   constexpr int kNext2 = (kSlot + 2) % kStages;
   constexpr int kPrev = (kSlot + kStages - 1) % kStages;
   const bool k2 = j + 2 < a.nT, v1 = j + 1 < a.nT;
   if (k2)
-    issue_half<false>(a.k_rsrc, a.k_row_bytes, lds.k[kNext2], (j + 2) * kTileKeys, a.wave, a.lane);
+    issue_half<Sh, false>(a.k_rsrc, a.k_row_bytes, lds.k[kNext2], (j + 2) * kTileKeys, a.wave,
+                          a.lane, a.d_chunks);
   if (v1)
-    issue_half<true>(a.v_rsrc, a.v_row_bytes, lds.v[kNext], (j + 1) * kTileKeys, a.wave, a.lane);
+    issue_half<Sh, true>(a.v_rsrc, a.v_row_bytes, lds.v[kNext], (j + 1) * kTileKeys, a.wave,
+                         a.lane, a.d_chunks);
   // Half 2j: P.V of half 2j-1 (V_{j-1}, keys 32..63), S of half 2j+1 (K_j, keys 32..63).
-  half_step<kPrev, 1, kSlot, 1, kSteady>(w, lds, 2 * j, a);
+  half_step<Sh, kPrev, 1, kSlot, 1, kSteady>(w, lds, 2 * j, a);
   // K_{j+1} and V_j were issued by step j-1; only this step's loads may still be in flight.
   if (k2 && v1)
-    wait_vmcnt<kLoadsPerWave>();
+    wait_vmcnt<Sh::kLoadsPerWave>();
   else if (k2 || v1)
-    wait_vmcnt<kLoadsPerWave / 2>();
+    wait_vmcnt<Sh::kLoadsPerWave / 2>();
   else
     wait_vmcnt<0>();
   lds_barrier();
   // Half 2j+1: P.V of half 2j (V_j, keys 0..31), S of half 2j+2 (K_{j+1}, keys 0..31).
-  half_step<kSlot, 0, kNext, 0, kSteady>(w, lds, 2 * j + 1, a);
+  half_step<Sh, kSlot, 0, kNext, 0, kSteady>(w, lds, 2 * j + 1, a);
 }
 
-// Element strides of one (B, H, N, 64) operand: batch, head, row (the last dim is contiguous).
+// Element strides of one (B, H, N, D) operand: batch, head, row (the last dim is contiguous).
 struct Strides {
   long long b, h, n;
 };
 
-// kDense: every operand is the contiguous (B, H, N, 64) layout, so row strides are the
-// compile-time 128 B and the stride arguments are not read (the tfgfa_fwd_bf16 case).
-template <bool kDense>
-__global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
-    const __bf16* __restrict__ Q, const __bf16* __restrict__ K, const __bf16* __restrict__ V,
-    __bf16* __restrict__ O, float* __restrict__ LSE, int H, int BH, int N, int nQB,
-    float scale_log2, int causal, Strides qs, Strides ks, Strides vs, Strides os) {
-  __shared__ __attribute__((aligned(1024))) unsigned char k0s[kHalfTileBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char k1s[kHalfTileBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char k2s[kHalfTileBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char v0s[kHalfTileBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char v1s[kHalfTileBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char v2s[kHalfTileBytes];
+// One instance per (head dims, element type, dim masking, layout).  kDense: every operand is
+// the contiguous (B, H, N, kD) layout with N_q = N_k, so row strides are compile-time and the
+// stride arguments are not read.
+template <class Sh, bool kDense>
+__global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 2 : 1) void fwd_kernel(
+    const void* __restrict__ Qv, const void* __restrict__ Kv, const void* __restrict__ Vv,
+    void* __restrict__ Ov, float* __restrict__ LSE, int H, int BH, int Nq, int Nk, int D,
+    int nQB, float scale_log2, int causal, Strides qs, Strides ks, Strides vs, Strides os) {
+  typedef typename Sh::T T;
+  typedef typename Elem<T>::v8 v8;
+  typedef typename Elem<T>::v4 v4;
+  constexpr int kSlotBytes = Sh::kDH * kHalfTileBytes;
+  constexpr int kDenseRowBytes = Sh::kD * 2;
+  __shared__ __attribute__((aligned(1024))) unsigned char k0s[kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char k1s[kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char k2s[kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char v0s[kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char v1s[kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char v2s[kSlotBytes];
   const Lds lds = {{k0s, k1s, k2s}, {v0s, v1s, v2s}};
+  const T* Q = static_cast<const T*>(Qv);
+  const T* K = static_cast<const T*>(Kv);
+  const T* V = static_cast<const T*>(Vv);
+  T* O = static_cast<T*>(Ov);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -399,54 +462,59 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
   const int bh = bid % BH;
 
   const int bb = bh / H, hh = bh - bb * H;
-  const long long dense_head = (long long)bh * N * kD;
-  const __bf16* Qh = kDense ? Q + dense_head : Q + bb * qs.b + hh * qs.h;
-  const int q_row_bytes = kDense ? kKRowBytes : (int)qs.n * 2;
+  const long long dense_head = (long long)bh * Nq * Sh::kD;
+  const T* Qh = kDense ? Q + dense_head : Q + bb * qs.b + hh * qs.h;
+  const int q_row_bytes = kDense ? kDenseRowBytes : (int)qs.n * 2;
 
   StepArgs a;
-  a.k_row_bytes = kDense ? kKRowBytes : (int)ks.n * 2;
-  a.v_row_bytes = kDense ? kKRowBytes : (int)vs.n * 2;
-  a.k_rsrc = head_desc(kDense ? K + dense_head : K + bb * ks.b + hh * ks.h, N, a.k_row_bytes);
-  a.v_rsrc = head_desc(kDense ? V + dense_head : V + bb * vs.b + hh * vs.h, N, a.v_row_bytes);
+  a.k_row_bytes = kDense ? kDenseRowBytes : (int)ks.n * 2;
+  a.v_row_bytes = kDense ? kDenseRowBytes : (int)vs.n * 2;
+  a.k_rsrc = head_desc(kDense ? K + dense_head : K + bb * ks.b + hh * ks.h, Nk, a.k_row_bytes);
+  a.v_rsrc = head_desc(kDense ? V + dense_head : V + bb * vs.b + hh * vs.h, Nk, a.v_row_bytes);
+  a.d_chunks = D >> 3;
   const int q0 = qb * kBlockRows + wave * kWaveRows;  // first query row of this wave
   const int qrow = q0 + r32;                          // this lane's query row
-  const int kv_end = causal ? min(N, (qb + 1) * kBlockRows) : N;
+  // Causal visibility is top-left aligned: query i sees keys j <= i (and j < Nk).
+  const int kv_end = causal ? min(Nk, (qb + 1) * kBlockRows) : Nk;
   a.nT = (kv_end + kTileKeys - 1) / kTileKeys;
   // 32-key halves computed by this wave: those starting at or below its first row (causal,
-  // q0 is a multiple of 32) and below N; unmasked: strictly below its first row (causal) and
-  // wholly below N.
-  const int nHalves = (min(N, kv_end) + 31) / 32;
-  if (q0 >= N) {
+  // q0 is a multiple of 32) and below Nk; unmasked: strictly below its first row (causal) and
+  // wholly below Nk.
+  const int nHalves = (kv_end + 31) / 32;
+  if (q0 >= Nq) {
     a.nAct = 0;
     a.nFull = 0;
   } else if (causal) {
     a.nAct = min(nHalves, q0 / 32 + 1);
-    a.nFull = min(q0 / 32, N / 32);
+    a.nFull = min(q0 / 32, Nk / 32);
   } else {
     a.nAct = nHalves;
-    a.nFull = N / 32;
+    a.nFull = Nk / 32;
   }
   a.nFull = min(a.nFull, a.nAct);
   a.wave = wave;
   a.lane = lane;
   a.h = h;
-  a.last_key = causal ? min(qrow, N - 1) : N - 1;
+  a.last_key = causal ? min(qrow, Nk - 1) : Nk - 1;
   a.scale_log2 = scale_log2;
 
   // Q first (ordinary buffer loads, tracked by the compiler), then the prologue tiles K_0, K_1
   // and V_0 (step j issues K_{j+2} and V_{j+1}).
-  WaveState w;
+  WaveState<Sh> w;
   {
     const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<__bf16*>(Qh), (short)0, N * q_row_bytes, 0x00020000);
+        const_cast<T*>(Qh), (short)0, Nq * q_row_bytes, 0x00020000);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      w.qop[c] = __builtin_bit_cast(
-          bf16x8, __builtin_amdgcn_raw_buffer_load_b128(qr, qrow * q_row_bytes + 32 * c + 16 * h, 0, 0));
+    for (int c = 0; c < 4 * Sh::kDH; ++c) {
+      int off = qrow * q_row_bytes + 32 * c + 16 * h;  // dims 16c + 8h .. +7
+      if (Sh::kMaskD) off = 2 * c + h < a.d_chunks ? off : kOutOfRange;
+      w.qop[c] = __builtin_bit_cast(v8, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+    }
   }
-  issue_half<false>(a.k_rsrc, a.k_row_bytes, lds.k[0], 0, wave, lane);
-  if (a.nT > 1) issue_half<false>(a.k_rsrc, a.k_row_bytes, lds.k[1], kTileKeys, wave, lane);
-  issue_half<true>(a.v_rsrc, a.v_row_bytes, lds.v[0], 0, wave, lane);
+  issue_half<Sh, false>(a.k_rsrc, a.k_row_bytes, lds.k[0], 0, wave, lane, a.d_chunks);
+  if (a.nT > 1)
+    issue_half<Sh, false>(a.k_rsrc, a.k_row_bytes, lds.k[1], kTileKeys, wave, lane, a.d_chunks);
+  issue_half<Sh, true>(a.v_rsrc, a.v_row_bytes, lds.v[0], 0, wave, lane, a.d_chunks);
 
   // K A-operand, d chunk c: row r32 (+32 for the second key half, an immediate), logical 16-B
   // chunk 2c + h.
@@ -467,10 +535,9 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
       }
   }
 #pragma unroll
-  for (int t = 0; t < 16; ++t) {
-    w.o0[t] = 0.f;
-    w.o1[t] = 0.f;
-  }
+  for (int i = 0; i < 2 * Sh::kDH; ++i)
+#pragma unroll
+    for (int t = 0; t < 16; ++t) w.o[i][t] = 0.f;
   w.m_run = -INFINITY;
   w.l_run = 0.f;
 
@@ -478,36 +545,36 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
   // (possibly NaN) meets the zeros.
   {
     uint4* vz = reinterpret_cast<uint4*>(lds.v[2]);
-    vz[tid] = make_uint4(0u, 0u, 0u, 0u);
-    vz[tid + kThreads] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int i = 0; i < kSlotBytes / 16 / kThreads; ++i) vz[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
   }
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc)
-    w.pb[cc] = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
+  for (int cc = 0; cc < 2; ++cc) w.pb[cc] = __builtin_bit_cast(v8, make_uint4(0u, 0u, 0u, 0u));
 
   // Wait for Q here, before the loop.  The compiler does not see the LDS transfers, so it
   // places a full vmcnt(0) before this use of the Q registers; that also covers K_0, K_1 and V_0
   // (once, in the prologue), and leaves no compiler-tracked loads whose waits could land inside
   // the loop and drain the transfers in flight there.
-  asm volatile("" ::"v"(w.qop[0]), "v"(w.qop[1]), "v"(w.qop[2]), "v"(w.qop[3]));
+#pragma unroll
+  for (int c = 0; c < 4 * Sh::kDH; ++c) asm volatile("" ::"v"(w.qop[c]));
   wait_vmcnt<0>();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   lds_barrier();
-  if (a.nAct > 0) w.s = qk_half<0, 0>(w, lds);
+  if (a.nAct > 0) w.s = qk_half<Sh, 0, 0>(w, lds);
 
   // Steady tile steps: both half-steps full (2j + 1 < nAct).
   const int nSteady = a.nAct / 2;
   int j = 0;
   for (; j + kStages <= nSteady; j += kStages) {
-    tile_step<0, true>(w, lds, j, a);
-    tile_step<1, true>(w, lds, j + 1, a);
-    tile_step<2, true>(w, lds, j + 2, a);
+    tile_step<Sh, 0, true>(w, lds, j, a);
+    tile_step<Sh, 1, true>(w, lds, j + 1, a);
+    tile_step<Sh, 2, true>(w, lds, j + 2, a);
   }
   if (j < nSteady) {
-    tile_step<0, true>(w, lds, j, a);
+    tile_step<Sh, 0, true>(w, lds, j, a);
     ++j;
     if (j < nSteady) {
-      tile_step<1, true>(w, lds, j, a);
+      tile_step<Sh, 1, true>(w, lds, j, a);
       ++j;
     }
   }
@@ -515,41 +582,41 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(
   for (; j < a.nT; ++j) {
     const int sl = j % kStages;
     if (sl == 0)
-      tile_step<0, false>(w, lds, j, a);
+      tile_step<Sh, 0, false>(w, lds, j, a);
     else if (sl == 1)
-      tile_step<1, false>(w, lds, j, a);
+      tile_step<Sh, 1, false>(w, lds, j, a);
     else
-      tile_step<2, false>(w, lds, j, a);
+      tile_step<Sh, 2, false>(w, lds, j, a);
   }
   // P.V of the last computed half when it is the second half of the last tile (V_{nT-1}
   // landed at the last step's barrier and its slot was not refilled): half-step 2nT.
   if (a.nAct == 2 * a.nT) {
     const int sl = (a.nT - 1) % kStages;
     if (sl == 0)
-      pv_half<0, 1>(w, lds);
+      pv_half<Sh, 0, 1>(w, lds);
     else if (sl == 1)
-      pv_half<1, 1>(w, lds);
+      pv_half<Sh, 1, 1>(w, lds);
     else
-      pv_half<2, 1>(w, lds);
+      pv_half<Sh, 2, 1>(w, lds);
   }
 
-  if (qrow < N) {
+  if (qrow < Nq) {
     const float inv_l = 1.0f / w.l_run;
-    __bf16* orow = kDense ? O + dense_head + (long long)qrow * kD
-                          : O + bb * os.b + hh * os.h + (long long)qrow * os.n;
+    T* orow = kDense ? O + dense_head + (long long)qrow * Sh::kD
+                     : O + bb * os.b + hh * os.h + (long long)qrow * os.n;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      bf16x4 lo4, hi4;
+    for (int i = 0; i < 2 * Sh::kDH; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        lo4[r] = (__bf16)(w.o0[4 * g + r] * inv_l);
-        hi4[r] = (__bf16)(w.o1[4 * g + r] * inv_l);
+      for (int g = 0; g < 4; ++g) {
+        // Register 4g + r of tile i holds dim 32i + 8g + 4h + r.
+        const int d0 = 32 * i + 8 * g + 4 * h;
+        v4 x;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = (T)(w.o[i][4 * g + r] * inv_l);
+        if (!Sh::kMaskD || d0 < D) *reinterpret_cast<v4*>(orow + d0) = x;
       }
-      *reinterpret_cast<bf16x4*>(orow + 8 * g + 4 * h) = lo4;
-      *reinterpret_cast<bf16x4*>(orow + 32 + 8 * g + 4 * h) = hi4;
-    }
     if (LSE != nullptr && h == 0) {
-      LSE[(size_t)bh * N + qrow] = (w.m_run + __builtin_amdgcn_logf(w.l_run)) * kLn2;
+      LSE[(size_t)bh * Nq + qrow] = (w.m_run + __builtin_amdgcn_logf(w.l_run)) * kLn2;
     }
   }
 }
@@ -569,28 +636,30 @@ static std::once_flag g_dev_once[kMaxDevices];
 static DeviceInfo g_dev_info[kMaxDevices];
 
 // Element strides of one operand as the kernel uses them.  A null `st` is the contiguous
-// (B, H, N, 64) layout.  The stride of a dimension of size 1 is never used (it may hold
-// anything, as in torch), so it is replaced by 0 (b, h) or 64 (n).
-static Strides operand_strides(const int64_t* st, int B, int H, int N) {
+// (B, H, N, D) layout.  The stride of a dimension of size 1 is never used (it may hold
+// anything, as in torch), so it is replaced by 0 (b, h) or D (n).
+static Strides operand_strides(const int64_t* st, int B, int H, int N, int D) {
   Strides s;
-  s.b = B == 1 ? 0 : st ? st[0] : (long long)H * N * kD;
-  s.h = H == 1 ? 0 : st ? st[1] : (long long)N * kD;
-  s.n = N == 1 ? kD : st ? st[2] : kD;
+  s.b = B == 1 ? 0 : st ? st[0] : (long long)H * N * D;
+  s.h = H == 1 ? 0 : st ? st[1] : (long long)N * D;
+  s.n = N == 1 ? D : st ? st[2] : D;
   return s;
 }
 
 // Stride rules (elements): the last dimension is dense (stride 1); the row stride is at least
-// 64, so rows of one head do not overlap and row N starts where a buffer descriptor over N
+// D, so rows of one head do not overlap and row N starts where a buffer descriptor over N
 // rows ends; every stride is a non-negative multiple of 8, so every row start keeps the
 // 16-byte alignment of the base pointer; the largest per-head buffer offset,
-// (N + 128) rows * row stride * 2 bytes, fits the 32-bit offset of a buffer access.
-static int check_strides(const int64_t* st, int B, int H, int N) {
-  if (st == nullptr) return TFGFA_OK;
-  if (st[3] != 1) return TFGFA_ERR_STRIDE;
-  const Strides s = operand_strides(st, B, H, N);
-  if (s.b < 0 || s.h < 0 || s.n < kD) return TFGFA_ERR_STRIDE;
-  if ((s.b | s.h | s.n) & 7) return TFGFA_ERR_STRIDE;
-  if (s.n > INT32_MAX / 2 || ((long long)N + kBlockRows) * s.n * 2 > INT32_MAX)
+// (N + 128) rows * row stride * 2 bytes + the row's 2 * 128 bytes, fits the 32-bit offset of
+// a buffer access.
+static int check_strides(const int64_t* st, int B, int H, int N, int D) {
+  const Strides s = operand_strides(st, B, H, N, D);
+  if (st != nullptr) {
+    if (st[3] != 1) return TFGFA_ERR_STRIDE;
+    if (s.b < 0 || s.h < 0 || s.n < D) return TFGFA_ERR_STRIDE;
+    if ((s.b | s.h | s.n) & 7) return TFGFA_ERR_STRIDE;
+  }
+  if (s.n > INT32_MAX / 2 || ((long long)N + kBlockRows) * s.n * 2 + 2 * kMaxD > INT32_MAX)
     return TFGFA_ERR_TOO_LARGE;
   return TFGFA_OK;
 }
@@ -598,9 +667,9 @@ static int check_strides(const int64_t* st, int B, int H, int N) {
 // O must not write one element twice: with its dimensions of size > 1 sorted by stride, each
 // stride must exceed the largest offset reachable through the smaller ones (a sufficient
 // condition for distinct offsets; every layout torch makes by viewing a buffer meets it).
-static bool overlaps(const int64_t* st, int B, int H, int N) {
+static bool overlaps(const int64_t* st, int B, int H, int N, int D) {
   if (st == nullptr) return false;
-  const Strides s = operand_strides(st, B, H, N);
+  const Strides s = operand_strides(st, B, H, N, D);
   long long stride[3] = {s.b, s.h, s.n};
   long long size[3] = {B, H, N};
   for (int i = 0; i < 3; ++i)  // insertion sort by stride, 3 elements
@@ -611,7 +680,7 @@ static bool overlaps(const int64_t* st, int B, int H, int N) {
       stride[j - 1] = ts;
       size[j - 1] = tz;
     }
-  long long reach = kD - 1;  // the dense last dimension
+  long long reach = D - 1;  // the dense last dimension
   for (int i = 0; i < 3; ++i) {
     if (size[i] == 1) continue;
     if (stride[i] <= reach) return true;
@@ -622,64 +691,128 @@ static bool overlaps(const int64_t* st, int B, int H, int N) {
 
 // Argument checks, in this order: sizes, flags and strides first, then - only for a non-empty
 // problem - pointers.  An empty tensor may legitimately have a null data pointer
-// (torch gives numel()==0 tensors address 0), so B, H or N == 0 succeeds with no launch.
+// (torch gives numel()==0 tensors address 0), so B, H or N_q == 0 succeeds with no launch.
 static int validate(const void* q, const void* k, const void* v, const void* o, const float* lse,
-                    int B, int H, int N, int D, float scale, int causal, const int64_t* const* st) {
-  if (B < 0 || H < 0 || N < 0) return TFGFA_ERR_BAD_SHAPE;
-  if (D != kD) return TFGFA_ERR_HEAD_DIM;
+                    int B, int H, int Nq, int Nk, int D, int dtype, float scale, int causal,
+                    const int64_t* const* st) {
+  if (B < 0 || H < 0 || Nq < 0 || Nk < 0) return TFGFA_ERR_BAD_SHAPE;
+  if (D < 8 || D > kMaxD || (D & 7)) return TFGFA_ERR_HEAD_DIM;
+  if (dtype != TFGFA_DTYPE_BF16 && dtype != TFGFA_DTYPE_F16) return TFGFA_ERR_DTYPE;
   if (!(scale > 0.f) || !isfinite(scale)) return TFGFA_ERR_SCALE;
   if (causal != 0 && causal != 1) return TFGFA_ERR_CAUSAL_FLAG;
-  if (B == 0 || H == 0 || N == 0) return TFGFA_OK;
+  if (B == 0 || H == 0 || Nq == 0) return TFGFA_OK;
+  if (Nk == 0) return TFGFA_ERR_BAD_SHAPE;  // every query row needs a key
   const long long bh = (long long)B * H;
-  const long long nqb = ((long long)N + kBlockRows - 1) / kBlockRows;
+  const long long nqb = ((long long)Nq + kBlockRows - 1) / kBlockRows;
   if (bh > INT32_MAX || bh * nqb > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
-  // Per-head byte offsets (row * 128 B for a contiguous head) are 32-bit buffer offsets.
-  if (((long long)N + kBlockRows) * kKRowBytes > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
+  const int rows[4] = {Nq, Nk, Nk, Nq};
   for (int i = 0; i < 4; ++i) {
-    const int sst = check_strides(st[i], B, H, N);
+    const int sst = check_strides(st[i], B, H, rows[i], D);
     if (sst != TFGFA_OK) return sst;
   }
-  if (overlaps(st[3], B, H, N)) return TFGFA_ERR_STRIDE;
+  if (overlaps(st[3], B, H, Nq, D)) return TFGFA_ERR_STRIDE;
   if (q == nullptr || k == nullptr || v == nullptr || o == nullptr) return TFGFA_ERR_NULL_POINTER;
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15u) return TFGFA_ERR_ALIGNMENT;
   if (((uintptr_t)lse) & 3u) return TFGFA_ERR_ALIGNMENT;
   return TFGFA_OK;
 }
 
-static int launch(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
-                  int N, int D, float softmax_scale, int causal, void* hip_stream,
-                  const int64_t* const* st) {
-  const int vst = validate(q, k, v, o, lse, B, H, N, D, softmax_scale, causal, st);
-  if (vst != TFGFA_OK) return vst;
-  if (B == 0 || H == 0 || N == 0) return TFGFA_OK;
+struct LaunchArgs {
+  const void *q, *k, *v;
+  void* o;
+  float* lse;
+  int H, BH, Nq, Nk, D, nQB;
+  float scale_log2;
+  int causal;
+  Strides qs, ks, vs, os;
+};
 
-  const int BH = B * H;
-  const int nQB = (N + kBlockRows - 1) / kBlockRows;
-  const float scale_log2 = softmax_scale * kLog2e;
-  const Strides qs = operand_strides(st[0], B, H, N), ks = operand_strides(st[1], B, H, N),
-                vs = operand_strides(st[2], B, H, N), os = operand_strides(st[3], B, H, N);
-  const Strides dense = operand_strides(nullptr, B, H, N);
+template <class Sh, bool kDense>
+static void launch_instance(const LaunchArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((fwd_kernel<Sh, kDense>), dim3(a.BH * a.nQB), dim3(kThreads), 0, stream, a.q,
+                     a.k, a.v, a.o, a.lse, a.H, a.BH, a.Nq, a.Nk, a.D, a.nQB, a.scale_log2,
+                     a.causal, a.qs, a.ks, a.vs, a.os);
+}
+
+template <int kD, typename T>
+static void launch_dims(const LaunchArgs& a, bool dense, hipStream_t stream) {
+  if (a.D != kD) {
+    launch_instance<Shape<kD, T, true>, false>(a, stream);
+    return;
+  }
+  if constexpr (kD == 64 && std::is_same<T, __bf16>::value) {
+    if (dense) {
+      launch_instance<Shape<kD, T, false>, true>(a, stream);  // the GPT-2 layout
+      return;
+    }
+  }
+  launch_instance<Shape<kD, T, false>, false>(a, stream);
+}
+
+static int launch(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
+                  int Nq, int Nk, int D, int dtype, float softmax_scale, int causal,
+                  void* hip_stream, const int64_t* const* st) {
+  const int vst = validate(q, k, v, o, lse, B, H, Nq, Nk, D, dtype, softmax_scale, causal, st);
+  if (vst != TFGFA_OK) return vst;
+  if (B == 0 || H == 0 || Nq == 0) return TFGFA_OK;
+
+  LaunchArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.H = H;
+  a.BH = B * H;
+  a.Nq = Nq;
+  a.Nk = Nk;
+  a.D = D;
+  a.nQB = (Nq + kBlockRows - 1) / kBlockRows;
+  a.scale_log2 = softmax_scale * kLog2e;
+  a.causal = causal;
+  a.qs = operand_strides(st[0], B, H, Nq, D);
+  a.ks = operand_strides(st[1], B, H, Nk, D);
+  a.vs = operand_strides(st[2], B, H, Nk, D);
+  a.os = operand_strides(st[3], B, H, Nq, D);
+  const Strides dq = operand_strides(nullptr, B, H, Nq, D);
   auto same = [](const Strides& x, const Strides& y) {
     return x.b == y.b && x.h == y.h && x.n == y.n;
   };
-  const bool all_dense = same(qs, dense) && same(ks, dense) && same(vs, dense) && same(os, dense);
-  hipLaunchKernelGGL(all_dense ? fwd_kernel<true> : fwd_kernel<false>, dim3(BH * nQB),
-                     dim3(kThreads), 0, (hipStream_t)hip_stream, static_cast<const __bf16*>(q),
-                     static_cast<const __bf16*>(k), static_cast<const __bf16*>(v),
-                     static_cast<__bf16*>(o), lse, H, BH, N, nQB, scale_log2, causal, qs, ks, vs,
-                     os);
+  const bool dense = Nq == Nk && same(a.qs, dq) && same(a.ks, dq) && same(a.vs, dq) && same(a.os, dq);
+  const hipStream_t stream = (hipStream_t)hip_stream;
+  if (dtype == TFGFA_DTYPE_BF16) {
+    if (D <= 64)
+      launch_dims<64, __bf16>(a, dense, stream);
+    else
+      launch_dims<128, __bf16>(a, dense, stream);
+  } else {
+    if (D <= 64)
+      launch_dims<64, _Float16>(a, dense, stream);
+    else
+      launch_dims<128, _Float16>(a, dense, stream);
+  }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? TFGFA_OK : -(int)e;
 }
 
 }  // namespace tfgfa
 
+extern "C" int tfgfa_fwd(const void* q, const int64_t* q_strides, const void* k,
+                         const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                         void* o, const int64_t* o_strides, float* lse, int B, int H, int N_q,
+                         int N_k, int D, int dtype, float softmax_scale, int causal,
+                         void* hip_stream) {
+  const int64_t* const st[4] = {q_strides, k_strides, v_strides, o_strides};
+  return tfgfa::launch(q, k, v, o, lse, B, H, N_q, N_k, D, dtype, softmax_scale, causal,
+                       hip_stream, st);
+}
+
 extern "C" int tfgfa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
                               int B, int H, int N, int D, float softmax_scale, int causal,
                               void* hip_stream) {
   const int64_t* const contiguous[4] = {nullptr, nullptr, nullptr, nullptr};
-  return tfgfa::launch(q, k, v, o, lse, B, H, N, D, softmax_scale, causal, hip_stream,
-                       contiguous);
+  return tfgfa::launch(q, k, v, o, lse, B, H, N, N, D, TFGFA_DTYPE_BF16, softmax_scale, causal,
+                       hip_stream, contiguous);
 }
 
 extern "C" int tfgfa_fwd_bf16_strided(const void* q, const int64_t* q_strides, const void* k,
@@ -688,22 +821,25 @@ extern "C" int tfgfa_fwd_bf16_strided(const void* q, const int64_t* q_strides, c
                                       const int64_t* o_strides, float* lse, int B, int H, int N,
                                       int D, float softmax_scale, int causal, void* hip_stream) {
   const int64_t* const st[4] = {q_strides, k_strides, v_strides, o_strides};
-  return tfgfa::launch(q, k, v, o, lse, B, H, N, D, softmax_scale, causal, hip_stream, st);
+  return tfgfa::launch(q, k, v, o, lse, B, H, N, N, D, TFGFA_DTYPE_BF16, softmax_scale, causal,
+                       hip_stream, st);
 }
 
 extern "C" const char* tfgfa_strerror(int status) {
   switch (status) {
     case TFGFA_OK: return "success";
     case TFGFA_ERR_NULL_POINTER: return "null tensor pointer (q, k, v and o are required)";
-    case TFGFA_ERR_BAD_SHAPE: return "negative batch, head or sequence size";
-    case TFGFA_ERR_HEAD_DIM: return "unsupported head dimension (only 64 is compiled)";
+    case TFGFA_ERR_BAD_SHAPE:
+      return "negative batch, head or sequence size, or no keys for a non-empty query";
+    case TFGFA_ERR_HEAD_DIM: return "unsupported head dimension (a multiple of 8 up to 128)";
+    case TFGFA_ERR_DTYPE: return "unsupported dtype (TFGFA_DTYPE_BF16 or TFGFA_DTYPE_F16)";
     case TFGFA_ERR_SCALE: return "softmax_scale must be finite and > 0";
     case TFGFA_ERR_CAUSAL_FLAG: return "causal flag must be 0 or 1";
     case TFGFA_ERR_TOO_LARGE: return "problem exceeds the launch limits (B*H*ceil(N/128) < 2^31)";
     case TFGFA_ERR_ALIGNMENT: return "misaligned pointer (q/k/v/o need 16 B, lse 4 B)";
     case TFGFA_ERR_CACHE: return "k_new/v_new (cache append) need cache_seqlens";
     case TFGFA_ERR_STRIDE:
-      return "unsupported strides (last dim 1; b, h, n non-negative multiples of 8; n >= 64; "
+      return "unsupported strides (last dim 1; b, h, n non-negative multiples of 8; n >= head dim; "
              "o without overlapping elements)";
     default: break;
   }

@@ -57,6 +57,24 @@ void fwd_strided(std::uintptr_t q, const Strides4& qs, std::uintptr_t k, const S
   }
 }
 
+void fwd_general(std::uintptr_t q, const Strides4& qs, std::uintptr_t k, const Strides4& ks,
+                 std::uintptr_t v, const Strides4& vs, std::uintptr_t o, const Strides4& os,
+                 std::uintptr_t lse, int B, int H, int N_q, int N_k, int D, int dtype,
+                 float softmax_scale, bool causal, std::uintptr_t stream) {
+  int st;
+  {
+    py::gil_scoped_release nogil;
+    st = tfgfa_fwd(reinterpret_cast<const void*>(q), qs.data(), reinterpret_cast<const void*>(k),
+                   ks.data(), reinterpret_cast<const void*>(v), vs.data(),
+                   reinterpret_cast<void*>(o), os.data(), reinterpret_cast<float*>(lse), B, H, N_q,
+                   N_k, D, dtype, softmax_scale, causal ? 1 : 0, reinterpret_cast<void*>(stream));
+  }
+  if (st != TFGFA_OK) {
+    throw std::runtime_error(std::string("tfgfa_fwd failed (status ") + std::to_string(st) +
+                             "): " + tfgfa_strerror(st));
+  }
+}
+
 using Strides3 = std::array<std::int64_t, 3>;
 
 void decode(std::uintptr_t q, const Strides3& qs, std::uintptr_t kc, const Strides4& ks,
@@ -110,6 +128,14 @@ PYBIND11_MODULE(_C, m) {
         py::arg("v_strides"), py::arg("o"), py::arg("o_strides"), py::arg("lse"), py::arg("B"),
         py::arg("H"), py::arg("N"), py::arg("D"), py::arg("softmax_scale"), py::arg("causal"),
         py::arg("stream"));
+  m.def("fwd_general", &fwd_general,
+        "Attention forward, any strides, bf16/fp16, head dim a multiple of 8 up to 128, N_q != N_k",
+        py::arg("q"), py::arg("q_strides"), py::arg("k"), py::arg("k_strides"), py::arg("v"),
+        py::arg("v_strides"), py::arg("o"), py::arg("o_strides"), py::arg("lse"), py::arg("B"),
+        py::arg("H"), py::arg("N_q"), py::arg("N_k"), py::arg("D"), py::arg("dtype"),
+        py::arg("softmax_scale"), py::arg("causal"), py::arg("stream"));
+  m.attr("DTYPE_BF16") = TFGFA_DTYPE_BF16;
+  m.attr("DTYPE_F16") = TFGFA_DTYPE_F16;
   m.def("decode", &decode,
         "One decode step over a KV cache on raw device pointers (element strides)",
         py::arg("q"), py::arg("q_strides"), py::arg("k_cache"), py::arg("k_strides"),

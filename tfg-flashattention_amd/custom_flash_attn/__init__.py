@@ -30,10 +30,12 @@ except ImportError as exc:  # pragma: no cover - exercised only on a broken buil
         f"({exc}); run `make -C tfg-flashattention_amd/csrc` or __graft_entry__.build()"
     ) from exc
 
-__all__ = ["forward", "forward_lse", "attention", "decode", "device_info", "HEAD_DIM",
-           "library_path"]
+__all__ = ["forward", "forward_lse", "attention", "flash_attn_forward", "decode", "device_info",
+           "HEAD_DIM", "MAX_HEAD_DIM", "library_path"]
 
-HEAD_DIM = 64  # the only compiled head dimension (common_types.hpp:33 fixes K = 64 too)
+HEAD_DIM = 64  # the head dimension of forward() (common_types.hpp:33 fixes K = 64 too)
+MAX_HEAD_DIM = 128  # attention() / flash_attn_forward(): any head dim up to 128
+_DTYPES = {torch.bfloat16: 0, torch.float16: 1}
 
 
 def library_path() -> str:
@@ -114,57 +116,96 @@ def forward_lse(Q: torch.Tensor, K_mat: torch.Tensor, V: torch.Tensor, /,
     return O, lse
 
 
-def _check_view(x, name: str, ref) -> None:
+def _check_view(x, name: str, ref, rows_from=None) -> None:
+    """A (B, H, N, D) view: CUDA, fp16/bf16 like ``ref``, same B, H, D (and N as
+    ``rows_from``, when given) and device, last dimension dense, D <= 128."""
     if not x.is_cuda:
         raise RuntimeError(f"{name} must be a CUDA tensor")
-    if x.dtype != torch.bfloat16:
-        raise RuntimeError("Unsupported tensor dtype. Use bfloat16.")
+    if x.dtype not in _DTYPES:
+        raise RuntimeError("Unsupported tensor dtype. Use bfloat16 or float16.")
     if x.dim() != 4:
         raise RuntimeError(f"{name} must be 4-D (batch, heads, seq_len, head_dim), got shape {tuple(x.shape)}")
     if ref is not None:
-        if x.shape != ref.shape:
-            raise RuntimeError(f"{name} must have shape {tuple(ref.shape)}, got {tuple(x.shape)}")
+        if x.dtype != ref.dtype:
+            raise RuntimeError(f"{name} must have dtype {ref.dtype}, got {x.dtype}")
+        want = (ref.shape[0], ref.shape[1], (rows_from if rows_from is not None else x).shape[2], ref.shape[3])
+        if tuple(x.shape) != tuple(want):
+            raise RuntimeError(f"{name} must have shape {tuple(want)}, got {tuple(x.shape)}")
         if x.device != ref.device:
             raise RuntimeError(f"{name} must be on {ref.device}, got {x.device}")
-    if x.shape[3] != HEAD_DIM:
-        raise RuntimeError(f"head_dim must be {HEAD_DIM}, got {x.shape[3]}")
+    if not 1 <= x.shape[3] <= MAX_HEAD_DIM:
+        raise RuntimeError(f"head_dim must be in [1, {MAX_HEAD_DIM}], got {x.shape[3]}")
     if x.stride(3) != 1 and x.shape[3] > 1:
         raise RuntimeError(f"{name} must be dense in its last dimension (stride 1), got strides {x.stride()}")
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, out: torch.Tensor | None = None,
               softmax_scale: float | None = None, causal: bool = True, return_lse: bool = False):
-    """Attention forward over strided (B, H, N, 64) bf16 views, with no copies.
+    """Attention forward over strided (B, H, N, D) views, with no copies.
 
-    ``q``, ``k``, ``v`` may be any views whose last dimension is dense, e.g. the
-    ``x.view(B, N, H, 64).transpose(1, 2)`` projections of a GPT-2 block
-    (src/py/model_inference.py:64-66), which the reference's caller copies with
-    ``.contiguous()`` first (:86-90).  ``out``, if given, is a (B, H, N, 64) bf16 view
-    the result is written into - pass ``buf.transpose(1, 2)`` of a (B, N, H, 64) buffer
-    and the (B, N, H*64) context needs no transposing copy (:92).  Batch, head and row
-    strides must be non-negative multiples of 8 elements with row stride >= 64 and data
-    16-byte aligned; other layouts raise RuntimeError from the C ABI.  Returns ``out``
-    (a new contiguous tensor when none is given), or ``(out, lse)`` with
-    ``return_lse=True`` (lse contiguous (B, H, N) float32, natural log).
+    ``q``: (B, H, N_q, D); ``k``, ``v``: (B, H, N_k, D); bf16 or fp16 (all alike); D up to 128;
+    any strides whose last dimension is dense, e.g. the ``x.view(B, N, H, D).transpose(1, 2)``
+    projections of a GPT-2 block (src/py/model_inference.py:64-66), which the reference's caller
+    copies with ``.contiguous()`` first (:86-90).  ``out``, if given, is a (B, H, N_q, D) view of
+    q's dtype the result is written into - pass ``buf.transpose(1, 2)`` of a (B, N, H, D) buffer
+    and the (B, N, H*D) context needs no transposing copy (:92).  ``causal`` masks top-left
+    aligned, as the reference's Triton kernel does (src/py/triton_implementation.py:127): query
+    i sees keys j <= i.  Batch, head and row strides must be non-negative multiples of 8
+    elements with row stride >= D and data 16-byte aligned; other layouts raise RuntimeError
+    from the C ABI.  A head dim that is not a multiple of 8 is zero-padded to one (a copy of
+    q, k, v), which leaves the scores unchanged.  Returns ``out`` (a new contiguous tensor
+    when none is given), or ``(out, lse)`` with ``return_lse=True`` (lse contiguous
+    (B, H, N_q) float32, natural log).
     """
     _check_view(q, "q", None)
     _check_view(k, "k", q)
-    _check_view(v, "v", q)
+    _check_view(v, "v", q, rows_from=k)
     if out is None:
         out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     else:
-        _check_view(out, "out", q)
-    B, H, N, D = q.shape
+        _check_view(out, "out", q, rows_from=q)
+    B, H, Nq, D = q.shape
+    Nk = k.shape[2]
     scale = (1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
-    lse = torch.empty((B, H, N), dtype=torch.float32, device=q.device) if return_lse else None
+    lse = torch.empty((B, H, Nq), dtype=torch.float32, device=q.device) if return_lse else None
+    if D % 8:
+        pad = 8 - D % 8
+        qp, kp, vp = (torch.nn.functional.pad(t, (0, pad)) for t in (q, k, v))
+        op = torch.empty(qp.shape, dtype=q.dtype, device=q.device)
+        _launch_general(qp, kp, vp, op, lse, scale, causal)
+        out.copy_(op[..., :D])
+    else:
+        _launch_general(q, k, v, out, lse, scale, causal)
+    return (out, lse) if return_lse else out
+
+
+def _launch_general(q, k, v, out, lse, scale, causal):
+    B, H, Nq, D = q.shape
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        _C.fwd_strided(
+        _C.fwd_general(
             q.data_ptr(), q.stride(), k.data_ptr(), k.stride(), v.data_ptr(), v.stride(),
             out.data_ptr(), out.stride(), 0 if lse is None else lse.data_ptr(),
-            B, H, N, D, scale, bool(causal), stream,
+            B, H, Nq, k.shape[2], D, _DTYPES[q.dtype], scale, bool(causal), stream,
         )
-    return (out, lse) if return_lse else out
+
+
+def flash_attn_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softmax_scale=None):
+    """Drop-in for the reference's Triton wrapper ``_flash_attn_forward(q, k, v, softmax_scale)``
+    (src/py/triton_implementation.py:184-241): causal attention of q (B, H, N_q, d) over k, v
+    (B, H, N_k, d), d <= 128, fp16 or bf16, scale ``softmax_scale or 1/sqrt(d)``; returns a new
+    O like q.  Argument errors are AssertionErrors with the wrapper's messages (:188-196).
+    """
+    batch, nheads, seqlen_q, d = q.shape
+    _, _, seqlen_k, _ = k.shape
+    assert k.shape == (batch, nheads, seqlen_k, d)
+    assert v.shape == (batch, nheads, seqlen_k, d)
+    assert d <= 128, "Flash Attention only supports head dimensions up to 128"
+    assert q.dtype == k.dtype == v.dtype, "All tensors must have the same type"
+    assert q.dtype in [torch.float16, torch.bfloat16], "Only supported types are fp16 and bf16"
+    softmax_scale = softmax_scale or 1.0 / math.sqrt(d)
+    o = torch.empty_like(q)
+    return attention(q, k, v, out=o, softmax_scale=softmax_scale, causal=True)
 
 
 def _check_vec(x, name: str, B: int, H: int, dev) -> None:
