@@ -238,8 +238,10 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     equals the last row of the causal forward over the first L tokens - what the reference's
     generate() recomputes from scratch for every token (src/py/model_inference.py:199-228).
     A length that does not fit the cache yields NaN for that batch row (checked on the device).
-    ``workspace``: optional uint8 device buffer for split-sequence partials; one of
-    ``_C.decode_workspace_bytes(B, H, N_max)`` bytes is allocated per call when absent.
+    ``workspace``: optional uint8 device buffer for split-sequence partials and completion
+    counters, zero-filled before its first use (each call leaves it zeroed); when absent, a
+    zeroed buffer of ``_C.decode_workspace_bytes(B, H, N_max)`` bytes is kept per device and
+    stream and reused.
     """
     for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
         if not t.is_cuda:
@@ -276,7 +278,7 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     scale = (1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
     lse = torch.empty((B, H), dtype=torch.float32, device=dev) if return_lse else None
     if workspace is None:
-        workspace = torch.empty(_C.decode_workspace_bytes(B, H, N_max), dtype=torch.uint8, device=dev)
+        workspace = _decode_workspace(dev, _C.decode_workspace_bytes(B, H, N_max))
     elif not workspace.is_cuda or workspace.device != dev or not workspace.is_contiguous():
         raise RuntimeError(f"workspace must be a contiguous tensor on {dev}")
     zero3 = (0, 0, 0)
@@ -294,6 +296,20 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
             workspace.numel() * workspace.element_size(), stream,
         )
     return (out, lse) if return_lse else out
+
+
+_WORKSPACES: dict = {}
+
+
+def _decode_workspace(dev, nbytes: int) -> torch.Tensor:
+    """A zeroed decode workspace of at least ``nbytes`` for (device, current stream), reused
+    across calls: the kernel leaves it zeroed, and calls on one stream do not overlap."""
+    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
 
 
 def device_info() -> dict:

@@ -176,7 +176,8 @@ class KVCache:
         self.seqlens = torch.zeros(batch, dtype=torch.int32, device=device)
         self.length = 0
         nbytes = custom_flash_attn._C.decode_workspace_bytes(batch, H, max_len)
-        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        # Split partials and completion counters; zeroed once, the kernel leaves it zeroed.
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=device)
 
     def advance(self, n: int) -> None:
         self.length += n
