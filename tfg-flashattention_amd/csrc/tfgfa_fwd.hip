@@ -17,12 +17,13 @@
 //   block first.
 //
 // Per-wave software pipeline (32-key halves u = 0, 1, ...)
-//   half-step u:  O += V_{u-1} P_{u-1}   together with   row max of S_u
-//                 (rescale O, l if some row max moved: wave-uniform branch)
-//                 S_{u+1} = K_{u+1} Q^T  together with   P_u = exp2(S_u - m), l += rowsum
-//   Each MFMA group shares a basic block with VALU work that does not depend on it, so the
-//   MFMA pipe and the VALU stay busy at the same time; the S double buffer is 2 x 16
-//   registers, which keeps three waves per SIMD.
+//   half-step u:  O += V_{u-1} P_{u-1}   interleaved with   P_u = exp2(S_u - m)
+//                 (move the offset m if some score passed it by the margin: rare branch)
+//                 S_{u+1} = K_{u+1} Q^T  interleaved with   row sums of P_u, P_u to bf16/fp16
+//   The steady half-step is a fixed sequence of chunks (one MFMA, the next operand read, a
+//   share of the VALU work) held in order by scheduling fences: a wave's VALU work overlaps
+//   its own in-flight MFMAs.  The S double buffer is 2 x 16 registers; 168 VGPRs keep three
+//   waves per SIMD at head dim 64.
 //
 // Memory pipeline
 //   K and V tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds: each lane's
@@ -57,8 +58,9 @@
 //   of a tile differ by an immediate offset.  V: swz = 2*(r & 3) makes the 4-row x 32-B footprint of a transposing read
 //   group (and of two groups side by side) hit distinct banks.
 //
-// Softmax runs in the exp2 domain: scores are scaled by scale*log2(e) inside one FMA, the
-// running max m and sum l are per-lane registers, and LSE = (m + log2 l) * ln 2.
+// Softmax runs in the exp2 domain: scores are scaled by scale*log2(e) inside one FMA; the
+// offset m and the sums l_run (fp32 probabilities) and l_p (rounded probabilities) are
+// per-lane registers; O = (P.V) / l_p and LSE = (m + log2 l_run) * ln 2.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -94,12 +96,11 @@ constexpr int kMaxD = 128;
 // returns zero without a memory access.  Used for head dims past D when D < the tile's dims.
 constexpr int kOutOfRange = 0x7FFFFFF0;
 
-// The exp2 offset is the exact running max of each row (moved whenever a half's max exceeds
-// it).  The row's largest score then gets probability exp2(0) = 1, which bf16 represents
-// exactly, so rounding P to bf16 for the MFMA leaves the dominant term of P.V exact; with a
-// lazier offset the dominant probability carries a 2^-9 relative error, which at GPT-2-XL
-// logit scales (sigma 3) costs up to ~1e-2 absolute in O.
-constexpr float kRescaleThreshold = 0.0f;
+// The exp2 offset m of a row moves (to the row's exact running max, rescaling O and the sums)
+// only when some score exceeds it by more than the element type's margin (log2 units), so
+// P <= 2^margin and the rescale is rare.  O is normalised by l_p, the sum of the probabilities
+// *as rounded* for the P.V MFMA, so the rounding of a dominant probability cancels between O's
+// numerator and denominator; the LSE uses l_run, the fp32 sum of the unrounded ones.
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -115,6 +116,18 @@ struct Elem<__bf16> {
   static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
+  // Offset margin (log2 units): P <= 2^64 keeps the fp32 sums finite for |V| * N < 2^64.
+  static constexpr float kMargin = 64.0f;
+  // acc + the sum of the 8 elements of p (exact products by 1, fp32 accumulation).
+  static __device__ __forceinline__ float sum8(v8 p, float acc) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 0, 1), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 2, 3), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 4, 5), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p, p, 6, 7), one, acc, false);
+    return acc;
+  }
 };
 template <>
 struct Elem<_Float16> {
@@ -122,6 +135,17 @@ struct Elem<_Float16> {
   typedef f16x4 v4;
   static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  // P <= 2^15 stays inside fp16's range (65504).
+  static constexpr float kMargin = 15.0f;
+  static __device__ __forceinline__ float sum8(v8 p, float acc) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 0, 1), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 2, 3), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 4, 5), one, acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(p, p, 6, 7), one, acc, false);
+    return acc;
   }
 };
 
@@ -245,8 +269,10 @@ struct WaveState {
   f32x16 o[2 * Sh::kDH]; // O^T accumulators: o[t] holds d = 32t .. 32t+31
   f32x16 s;              // S^T of the half being softmaxed: register t = key 8(t/4) + 4h + t%4
   v8 pb[2];              // P^T of the previous half, waiting for its P.V
-  float m_run;           // exp2 offset (running max of scale*log2e*s)
-  float l_run;           // running sum of exp2(scale*log2e*s - m_run)
+  float m_run;           // exp2 offset (a running max of scale*log2e*s, moved lazily)
+  float thr;             // raw score above which the offset has to move: (m_run + margin) / (scale*log2e)
+  float l_run;           // this lane's running sum of exp2(scale*log2e*s - m_run) (fp32, for the LSE)
+  float l_p;             // this lane's running sum of the same probabilities rounded to T (for O)
   int koff[4];           // K A-operand LDS offsets (within a K dim half, key half 0)
   int voff[2][2];        // V^T transposing-read LDS offsets (within a V dim half, keys 0..15)
 };
@@ -305,27 +331,30 @@ __device__ __forceinline__ void mask_half(WaveState<Sh>& w, int lim) {
   }
 }
 
-// Row max of w.s over the lane pair, scaled to the exp2 domain.
+// Max of this lane's 16 raw scores.
 template <class Sh>
-__device__ __forceinline__ float row_max(const WaveState<Sh>& w, float scale_log2) {
+__device__ __forceinline__ float lane_max(const WaveState<Sh>& w) {
   float mx = fmaxf(w.s[0], fmaxf(w.s[1], w.s[2]));
 #pragma unroll
-  for (int t = 3; t < 15; t += 2) mx = fmaxf(mx, fmaxf(w.s[t], w.s[t + 1]));
-  mx = fmaxf(mx, w.s[15]);
-  return pair_max(mx) * scale_log2;
+  for (int t = 3; t < 15; t += 2) mx = fmaxf(fmaxf(mx, w.s[t]), w.s[t + 1]);
+  return fmaxf(mx, w.s[15]);
 }
 
-// Rescale of O and l when some row's max moved (skipped, wave-uniformly, when none did).
-// Every computed half has an unmasked key in every row (it starts at or below the wave's first
-// row), so the max is finite and the first half always moves m_run off -inf.
+// Moves the exp2 offset of every row to its exact running max, rescaling O and the sums, when
+// some lane's score exceeds its row's offset by more than the margin (wave-uniform branch, taken
+// at a wave's first half and then rarely).  Every computed half has an unmasked key in every
+// row (it starts at or below the wave's first row), so the pair max is finite and the first
+// half always moves m_run off -inf.
 template <class Sh>
-__device__ __forceinline__ void rescale(WaveState<Sh>& w, float m_tile) {
-  const bool grow = m_tile > w.m_run + kRescaleThreshold;
-  if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-    const float m_new = grow ? m_tile : w.m_run;
+__device__ __forceinline__ void move_offset(WaveState<Sh>& w, float mx, float scale_log2,
+                                            float inv_scale_log2) {
+  if (__builtin_amdgcn_ballot_w64(mx > w.thr) != 0) {
+    const float m_new = fmaxf(w.m_run, pair_max(mx) * scale_log2);
     const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
     w.m_run = m_new;
+    w.thr = (m_new + Elem<typename Sh::T>::kMargin) * inv_scale_log2;
     w.l_run *= alpha;
+    w.l_p *= alpha;
 #pragma unroll
     for (int i = 0; i < 2 * Sh::kDH; ++i)
 #pragma unroll
@@ -333,27 +362,149 @@ __device__ __forceinline__ void rescale(WaveState<Sh>& w, float m_tile) {
   }
 }
 
-// P = exp2(scale*log2e*s - m_run) in fp32, row sum into l (two partial sums), P rounded to
-// the element type into w.pb: chunk cc (keys 16cc .. 16cc+15 of the half) is registers
-// 8cc .. 8cc+7.
+// Sum of the probabilities p into l_run, p rounded to the element type into w.pb (chunk cc =
+// keys 16cc .. 16cc+15 of the half: registers 8cc .. 8cc+7), the sum of the rounded values
+// into l_p.
+template <class Sh, class P>
+__device__ __forceinline__ void sum_convert(WaveState<Sh>& w, const P& p) {
+  typedef typename Sh::T T;
+  float ps0 = p[0], ps1 = p[1];
+#pragma unroll
+  for (int t = 2; t < 16; t += 2) {
+    ps0 += p[t];
+    ps1 += p[t + 1];
+  }
+  w.l_run += ps0 + ps1;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    w.pb[0][e] = (T)p[e];
+    w.pb[1][e] = (T)p[8 + e];
+  }
+  w.l_p = Elem<T>::sum8(w.pb[1], Elem<T>::sum8(w.pb[0], w.l_p));
+}
+
+// P = exp2(scale*log2e*s - m_run) in fp32 (in place), then sum_convert.
 template <class Sh>
 __device__ __forceinline__ void exp_half(WaveState<Sh>& w, float scale_log2) {
-  typedef typename Sh::T T;
   const float neg_m = -w.m_run;
 #pragma unroll
   for (int t = 0; t < 16; ++t) w.s[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, neg_m));
-  float ps0 = w.s[0], ps1 = w.s[1];
+  sum_convert(w, w.s);
+}
+
+template <class Sh, int kVs, int kVh>
+__device__ __forceinline__ typename Elem<typename Sh::T>::v8 v_operand(const WaveState<Sh>& w,
+                                                                      const Lds& lds, int i) {
+  typedef typename Elem<typename Sh::T>::v8 v8;
+  const int dh = i >> 2, cc = (i >> 1) & 1, dt = i & 1;
+  const unsigned char* vt =
+      lds.v[kVs] + dh * kHalfTileBytes + kVh * 32 * kKRowBytes + cc * 16 * kKRowBytes;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(vt + w.voff[dt][0]));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(vt + w.voff[dt][1]));
+  return __builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+template <class Sh, int kKs, int kKh>
+__device__ __forceinline__ typename Elem<typename Sh::T>::v8 k_operand(const WaveState<Sh>& w,
+                                                                      const Lds& lds, int i) {
+  typedef typename Elem<typename Sh::T>::v8 v8;
+  const int dh = i >> 2, c = i & 3;
+  const unsigned char* kt = lds.k[kKs] + dh * kHalfTileBytes + kKh * 32 * kKRowBytes;
+  return *reinterpret_cast<const v8*>(kt + w.koff[c]);
+}
+
+#define TFGFA_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+// A full half-step u as a fixed sequence of chunks, each MFMA followed by a share of the VALU
+// work that does not depend on it (a wave's VALU work overlaps its own in-flight MFMAs):
+//   chunk 0          V^T operands of the first two P.V MFMAs; lane max of S_u and the
+//                    offset check
+//   chunks 1..kPv    MFMA i of O += V_{u-1} P_{u-1}, the next operand read, a share of
+//                    P_u = exp2(scale*log2e*S_u - m_run)
+//   (rare branch)    move the offset: rescale O and the sums, recompute P_u (the chunks'
+//                    exps stay in their chunks: each is pinned there by an empty asm)
+//   chunks kPv+1..   MFMA i of S_{u+1} = K_{u+1} Q^T, the next operand read, a share of
+//                    the sums of P_u and its conversion to the element type
+template <class Sh, int kVs, int kVh, int kKs, int kKh>
+__device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, float scale_log2,
+                                           float inv_scale_log2) {
+  typedef typename Sh::T T;
+  typedef typename Elem<T>::v8 v8;
+  constexpr int kPv = 4 * Sh::kDH;
+  constexpr int kS = 4 * Sh::kDH;
+  v8 vop[2];
+  vop[0] = v_operand<Sh, kVs, kVh>(w, lds, 0);
+  vop[1] = v_operand<Sh, kVs, kVh>(w, lds, 1);
+  const float mx = lane_max(w);
+  const bool move = __builtin_amdgcn_ballot_w64(mx > w.thr) != 0;
+  TFGFA_FENCE();
+  const float neg_m = -w.m_run;
+  float p[16];
+  v8 kop[2];
 #pragma unroll
-  for (int t = 2; t < 16; t += 2) {
-    ps0 += w.s[t];
-    ps1 += w.s[t + 1];
-  }
-  w.l_run += pair_sum(ps0 + ps1);
+  for (int i = 0; i < kPv; ++i) {
+    const int dh = i >> 2, cc = (i >> 1) & 1, dt = i & 1;
+    w.o[2 * dh + dt] = Elem<T>::mfma(vop[i & 1], w.pb[cc], w.o[2 * dh + dt]);
+    if (i + 2 < kPv)
+      vop[i & 1] = v_operand<Sh, kVs, kVh>(w, lds, i + 2);
+    else
+      kop[i + 2 - kPv] = k_operand<Sh, kKs, kKh>(w, lds, i + 2 - kPv);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    w.pb[0][e] = (T)w.s[e];
-    w.pb[1][e] = (T)w.s[8 + e];
+    for (int t = 16 * i / kPv; t < 16 * (i + 1) / kPv; ++t)
+      p[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, neg_m));
+    // Computed here, in this chunk, even though the rare branch below recomputes them.
+#pragma unroll
+    for (int t = 16 * i / kPv; t < 16 * (i + 1) / kPv; ++t) asm volatile("" : "+v"(p[t]));
+    TFGFA_FENCE();
   }
+  if (move) {
+    const float m_new = fmaxf(w.m_run, pair_max(mx) * scale_log2);
+    const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
+    w.m_run = m_new;
+    w.thr = (m_new + Elem<typename Sh::T>::kMargin) * inv_scale_log2;
+    w.l_run *= alpha;
+    w.l_p *= alpha;
+#pragma unroll
+    for (int i = 0; i < 2 * Sh::kDH; ++i)
+#pragma unroll
+      for (int t = 0; t < 16; ++t) w.o[i][t] *= alpha;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) p[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, -m_new));
+  }
+  f32x16 acc;
+#pragma unroll
+  for (int t = 0; t < 16; ++t) acc[t] = 0.f;
+  float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kS; ++i) {
+    acc = Elem<T>::mfma(kop[i & 1], w.qop[i], acc);
+    if (i + 2 < kS) kop[i & 1] = k_operand<Sh, kKs, kKh>(w, lds, i + 2);
+    if (i == 0) {
+      ps0 = p[0];
+      ps1 = p[1];
+#pragma unroll
+      for (int t = 2; t < 16; t += 2) {
+        ps0 += p[t];
+        ps1 += p[t + 1];
+      }
+      w.l_run += ps0 + ps1;
+      asm volatile("" : "+v"(w.l_run));
+    } else if (i == 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        w.pb[0][e] = (T)p[e];
+        w.pb[1][e] = (T)p[8 + e];
+      }
+      asm volatile("" : "+v"(w.pb[0]), "+v"(w.pb[1]));
+    } else if (i == 2) {
+      w.l_p = Elem<T>::sum8(w.pb[1], Elem<T>::sum8(w.pb[0], w.l_p));
+      asm volatile("" : "+v"(w.l_p));
+    }
+    TFGFA_FENCE();
+  }
+  w.s = acc;
 }
 
 // Loop-invariant inputs of the pipeline.
@@ -365,7 +516,7 @@ struct StepArgs {
   int nAct;      // 32-key halves this wave computes (a prefix)
   int nFull;     // halves this wave computes without an element mask (a prefix of the above)
   int wave, lane, h, last_key;
-  float scale_log2;
+  float scale_log2, inv_scale_log2;
 };
 
 // Half-step u: P.V of half u-1 (V slot kVs, half kVh), softmax of half u, S of half u+1 (K
@@ -380,10 +531,14 @@ __device__ __forceinline__ void half_step(WaveState<Sh>& w, const Lds& lds, int 
                                           const StepArgs& a) {
   if (!kSteady && u > a.nAct) return;
   if (u >= a.nFull && u < a.nAct) mask_half(w, a.last_key - u * 32 - 4 * a.h);
+  if (kSteady) {
+    fused_step<Sh, kVs, kVh, kKs, kKh>(w, lds, a.scale_log2, a.inv_scale_log2);
+    return;
+  }
   pv_half<Sh, kVs, kVh>(w, lds);
-  const float m_tile = row_max(w, a.scale_log2);
+  const float mx = lane_max(w);
   if (!kSteady && u == a.nAct) return;
-  rescale(w, m_tile);
+  move_offset(w, mx, a.scale_log2, a.inv_scale_log2);
   const f32x16 n = qk_half<Sh, kKs, kKh>(w, lds);
   exp_half(w, a.scale_log2);
   w.s = n;
@@ -427,7 +582,7 @@ struct Strides {
 // the contiguous (B, H, N, kD) layout with N_q = N_k, so row strides are compile-time and the
 // stride arguments are not read.
 template <class Sh, bool kDense>
-__global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 2 : 1) void fwd_kernel(
+__global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 1) void fwd_kernel(
     const void* __restrict__ Qv, const void* __restrict__ Kv, const void* __restrict__ Vv,
     void* __restrict__ Ov, float* __restrict__ LSE, int H, int BH, int Nq, int Nk, int D,
     int nQB, float scale_log2, int causal, Strides qs, Strides ks, Strides vs, Strides os) {
@@ -497,6 +652,7 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 2 : 1) void fwd_kernel(
   a.h = h;
   a.last_key = causal ? min(qrow, Nk - 1) : Nk - 1;
   a.scale_log2 = scale_log2;
+  a.inv_scale_log2 = 1.0f / scale_log2;
 
   // Q first (ordinary buffer loads, tracked by the compiler), then the prologue tiles K_0, K_1
   // and V_0 (step j issues K_{j+2} and V_{j+1}).
@@ -539,7 +695,9 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 2 : 1) void fwd_kernel(
 #pragma unroll
     for (int t = 0; t < 16; ++t) w.o[i][t] = 0.f;
   w.m_run = -INFINITY;
+  w.thr = -INFINITY;
   w.l_run = 0.f;
+  w.l_p = 0.f;
 
   // Half-step 0 runs a P.V against V slot 2 with P = 0: zero that slot so no stale LDS value
   // (possibly NaN) meets the zeros.
@@ -600,8 +758,11 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 2 : 1) void fwd_kernel(
       pv_half<Sh, 2, 1>(w, lds);
   }
 
+  // Row sums over the lane pair (both lanes of a row hold the same offset).
+  const float l_o = pair_sum(w.l_p);
+  const float l_all = pair_sum(w.l_run);
   if (qrow < Nq) {
-    const float inv_l = 1.0f / w.l_run;
+    const float inv_l = 1.0f / l_o;
     T* orow = kDense ? O + dense_head + (long long)qrow * Sh::kD
                      : O + bb * os.b + hh * os.h + (long long)qrow * os.n;
 #pragma unroll
@@ -616,7 +777,7 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 2 : 1) void fwd_kernel(
         if (!Sh::kMaskD || d0 < D) *reinterpret_cast<v4*>(orow + d0) = x;
       }
     if (LSE != nullptr && h == 0) {
-      LSE[(size_t)bh * Nq + qrow] = (w.m_run + __builtin_amdgcn_logf(w.l_run)) * kLn2;
+      LSE[(size_t)bh * Nq + qrow] = (w.m_run + __builtin_amdgcn_logf(l_all)) * kLn2;
     }
   }
 }
