@@ -27,10 +27,12 @@
 //
 // Memory pipeline
 //   K and V tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds: each lane's
-//   16 B land at LDS base + 16*lane), no registers or VALU spent on staging.  Two rings of 3
-//   slots (K, V).  Tile step j: issue K_{j+2} and V_{j+1}; half-step 2j (uses K_j, V_{j-1});
-//   wait for this wave's loads of K_{j+1} and V_j and barrier; half-step 2j+1 (uses K_{j+1},
-//   V_j).  The barrier also proves every wave has finished with the slots refilled at step j+1.
+//   16 B land at LDS base + 16*lane), no registers or VALU spent on staging.  A ring of 3 K
+//   slots and a ring of 3 (head dim 64) or 2 (head dim 128) V slots.  Tile step j: issue
+//   K_{j+2} (and V_{j+1} with 3 V slots); half-step 2j (uses K_j, V_{j-1}); wait for this
+//   wave's loads of K_{j+1} and V_j and barrier; (2 V slots: issue V_{j+1} into V_{j-1}'s
+//   slot); half-step 2j+1 (uses K_{j+1}, V_j).  The barrier also proves every wave has
+//   finished with the slots refilled after it.
 //   Loads past the sequence end return zero (buffer range check): the zero-fill of partial
 //   tiles.
 //
@@ -90,7 +92,7 @@ constexpr int kBlockRows = kWaves * kWaveRows;  // 128 query rows per workgroup
 constexpr int kTileKeys = 64;               // keys per K/V tile
 constexpr int kKRowBytes = kDHalf * 2;      // 128 B per key row of one dim half in LDS
 constexpr int kHalfTileBytes = kTileKeys * kKRowBytes;  // 8 KiB (K or V, one dim half)
-constexpr int kStages = 3;
+constexpr int kStages = 3;  // K ring slots (the V ring has Shape::kVSlots: 3 or 2)
 constexpr int kMaxD = 128;
 // A buffer offset past any num_records built here (those stay below 2^31 - 2^24): the load
 // returns zero without a memory access.  Used for head dims past D when D < the tile's dims.
@@ -214,7 +216,15 @@ struct Shape {
   static constexpr bool kMaskD = kMaskD_;
   typedef T_ T;
   static constexpr int kLoadsPerWave = 4 * kDH;  // transfers per tile step per wave (K and V)
+  // V ring slots.  3: V_{j+1} is issued at the start of tile step j.  2: V_{j+1} is issued after
+  // step j's barrier, into the slot of V_{j-1} (read by half-step 2j, before the barrier); the
+  // rings then take 5 slots of LDS instead of 6.  Head dim 128 uses 2: 80 KiB of LDS per
+  // workgroup, so two workgroups (two waves per SIMD) fit a CU's 160 KiB.
+  static constexpr int kVSlots = kD_ == 128 ? 2 : 3;
+  // Tile steps after which the K and V slot assignments repeat.
+  static constexpr int kPeriod = kVSlots == 3 ? 3 : 6;
   static_assert(kD_ == 64 || kD_ == 128, "compiled head dims");
+  static_assert(kVSlots == 2 || kVSlots == 3, "V ring slots");
 };
 
 // This wave's share of one K (or V) tile: rows [8*(2w), 8*(2w+2)) of each dim half as two
@@ -258,7 +268,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // dim halves.
 struct Lds {
   unsigned char* k[kStages];
-  unsigned char* v[kStages];
+  unsigned char* v[3];
 };
 
 // Per-wave state carried across half-steps.
@@ -544,33 +554,75 @@ __device__ __forceinline__ void half_step(WaveState<Sh>& w, const Lds& lds, int 
   w.s = n;
 }
 
-// Tile step j (slot kSlot = j % 3): issue K_{j+2}, V_{j+1}; half-step 2j; wait for K_{j+1} and
-// V_j; barrier; half-step 2j+1.
-template <class Sh, int kSlot, bool kSteady>
+// Tile step j (K slot kKs = j % 3, V slot kVs = j % kVSlots): issue K_{j+2} (and, with a 3-slot
+// V ring, V_{j+1}); half-step 2j; wait for K_{j+1} and V_j; barrier; (2-slot V ring: issue
+// V_{j+1}); half-step 2j+1.
+template <class Sh, int kKs, int kVs, bool kSteady>
 __device__ __forceinline__ void tile_step(WaveState<Sh>& w, const Lds& lds, int j,
                                           const StepArgs& a) {
-  constexpr int kNext = (kSlot + 1) % kStages;
-  constexpr int kNext2 = (kSlot + 2) % kStages;
-  constexpr int kPrev = (kSlot + kStages - 1) % kStages;
+  constexpr int kKNext = (kKs + 1) % kStages;
+  constexpr int kKNext2 = (kKs + 2) % kStages;
+  constexpr int kVN = Sh::kVSlots;
+  constexpr int kVPrev = (kVs + kVN - 1) % kVN;  // V_{j-1}
+  constexpr int kVNext = (kVs + 1) % kVN;        // V_{j+1}
   const bool k2 = j + 2 < a.nT, v1 = j + 1 < a.nT;
   if (k2)
-    issue_half<Sh, false>(a.k_rsrc, a.k_row_bytes, lds.k[kNext2], (j + 2) * kTileKeys, a.wave,
+    issue_half<Sh, false>(a.k_rsrc, a.k_row_bytes, lds.k[kKNext2], (j + 2) * kTileKeys, a.wave,
                           a.lane, a.d_chunks);
-  if (v1)
-    issue_half<Sh, true>(a.v_rsrc, a.v_row_bytes, lds.v[kNext], (j + 1) * kTileKeys, a.wave,
+  if (kVN == 3 && v1)
+    issue_half<Sh, true>(a.v_rsrc, a.v_row_bytes, lds.v[kVNext], (j + 1) * kTileKeys, a.wave,
                          a.lane, a.d_chunks);
   // Half 2j: P.V of half 2j-1 (V_{j-1}, keys 32..63), S of half 2j+1 (K_j, keys 32..63).
-  half_step<Sh, kPrev, 1, kSlot, 1, kSteady>(w, lds, 2 * j, a);
+  half_step<Sh, kVPrev, 1, kKs, 1, kSteady>(w, lds, 2 * j, a);
   // K_{j+1} and V_j were issued by step j-1; only this step's loads may still be in flight.
-  if (k2 && v1)
+  if (kVN == 3 && k2 && v1)
     wait_vmcnt<Sh::kLoadsPerWave>();
-  else if (k2 || v1)
+  else if (k2 || (kVN == 3 && v1))
     wait_vmcnt<Sh::kLoadsPerWave / 2>();
   else
     wait_vmcnt<0>();
   lds_barrier();
+  if (kVN == 2 && v1)
+    issue_half<Sh, true>(a.v_rsrc, a.v_row_bytes, lds.v[kVNext], (j + 1) * kTileKeys, a.wave,
+                         a.lane, a.d_chunks);
   // Half 2j+1: P.V of half 2j (V_j, keys 0..31), S of half 2j+2 (K_{j+1}, keys 0..31).
-  half_step<Sh, kSlot, 0, kNext, 0, kSteady>(w, lds, 2 * j + 1, a);
+  half_step<Sh, kVs, 0, kKNext, 0, kSteady>(w, lds, 2 * j + 1, a);
+}
+
+// Tile step j with its slots chosen at run time (j % kPeriod).
+template <class Sh, bool kSteady, int kP = 0>
+__device__ __forceinline__ void tile_step_at(WaveState<Sh>& w, const Lds& lds, int j,
+                                             const StepArgs& a) {
+  if constexpr (kP < Sh::kPeriod) {
+    if (j % Sh::kPeriod == kP)
+      tile_step<Sh, kP % kStages, kP % Sh::kVSlots, kSteady>(w, lds, j, a);
+    else
+      tile_step_at<Sh, kSteady, kP + 1>(w, lds, j, a);
+  }
+}
+
+// kPeriod steady tile steps j0 .. j0 + kPeriod - 1 (j0 a multiple of kPeriod), slots at
+// compile time.
+template <class Sh, int kP = 0>
+__device__ __forceinline__ void steady_period(WaveState<Sh>& w, const Lds& lds, int j0,
+                                              const StepArgs& a) {
+  if constexpr (kP < Sh::kPeriod) {
+    tile_step<Sh, kP % kStages, kP % Sh::kVSlots, true>(w, lds, j0 + kP, a);
+    steady_period<Sh, kP + 1>(w, lds, j0, a);
+  }
+}
+
+// The steady tile steps j0 .. n - 1 of a partial period (n - j0 < kPeriod), slots at compile
+// time.
+template <class Sh, int kP = 0>
+__device__ __forceinline__ void steady_rest(WaveState<Sh>& w, const Lds& lds, int j0, int n,
+                                            const StepArgs& a) {
+  if constexpr (kP + 1 < Sh::kPeriod) {
+    if (j0 + kP < n) {
+      tile_step<Sh, kP % kStages, kP % Sh::kVSlots, true>(w, lds, j0 + kP, a);
+      steady_rest<Sh, kP + 1>(w, lds, j0, n, a);
+    }
+  }
 }
 
 // Element strides of one (B, H, N, D) operand: batch, head, row (the last dim is contiguous).
@@ -582,7 +634,7 @@ struct Strides {
 // the contiguous (B, H, N, kD) layout with N_q = N_k, so row strides are compile-time and the
 // stride arguments are not read.
 template <class Sh, bool kDense>
-__global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 1) void fwd_kernel(
+__global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
     const void* __restrict__ Qv, const void* __restrict__ Kv, const void* __restrict__ Vv,
     void* __restrict__ Ov, float* __restrict__ LSE, int H, int BH, int Nq, int Nk, int D,
     int nQB, float scale_log2, int causal, Strides qs, Strides ks, Strides vs, Strides os) {
@@ -594,10 +646,9 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 1) void fwd_kernel(
   __shared__ __attribute__((aligned(1024))) unsigned char k0s[kSlotBytes];
   __shared__ __attribute__((aligned(1024))) unsigned char k1s[kSlotBytes];
   __shared__ __attribute__((aligned(1024))) unsigned char k2s[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char v0s[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char v1s[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char v2s[kSlotBytes];
-  const Lds lds = {{k0s, k1s, k2s}, {v0s, v1s, v2s}};
+  __shared__ __attribute__((aligned(1024))) unsigned char vring[Sh::kVSlots * kSlotBytes];
+  const Lds lds = {{k0s, k1s, k2s},
+                   {vring, vring + kSlotBytes, vring + (Sh::kVSlots - 1) * kSlotBytes}};
   const T* Q = static_cast<const T*>(Qv);
   const T* K = static_cast<const T*>(Kv);
   const T* V = static_cast<const T*>(Vv);
@@ -699,10 +750,10 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 1) void fwd_kernel(
   w.l_run = 0.f;
   w.l_p = 0.f;
 
-  // Half-step 0 runs a P.V against V slot 2 with P = 0: zero that slot so no stale LDS value
-  // (possibly NaN) meets the zeros.
+  // Half-step 0 runs a P.V against the last V slot (that of V_{-1}) with P = 0: zero that
+  // slot so no stale LDS value (possibly NaN) meets the zeros.
   {
-    uint4* vz = reinterpret_cast<uint4*>(lds.v[2]);
+    uint4* vz = reinterpret_cast<uint4*>(lds.v[Sh::kVSlots - 1]);
 #pragma unroll
     for (int i = 0; i < kSlotBytes / 16 / kThreads; ++i) vz[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
   }
@@ -723,33 +774,15 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 1) void fwd_kernel(
   // Steady tile steps: both half-steps full (2j + 1 < nAct).
   const int nSteady = a.nAct / 2;
   int j = 0;
-  for (; j + kStages <= nSteady; j += kStages) {
-    tile_step<Sh, 0, true>(w, lds, j, a);
-    tile_step<Sh, 1, true>(w, lds, j + 1, a);
-    tile_step<Sh, 2, true>(w, lds, j + 2, a);
-  }
-  if (j < nSteady) {
-    tile_step<Sh, 0, true>(w, lds, j, a);
-    ++j;
-    if (j < nSteady) {
-      tile_step<Sh, 1, true>(w, lds, j, a);
-      ++j;
-    }
-  }
+  for (; j + Sh::kPeriod <= nSteady; j += Sh::kPeriod) steady_period<Sh>(w, lds, j, a);
+  steady_rest<Sh>(w, lds, j, nSteady, a);
+  j = max(j, nSteady);
   // Remaining tile steps (the wave's last half and P.V, then loads and barriers only).
-  for (; j < a.nT; ++j) {
-    const int sl = j % kStages;
-    if (sl == 0)
-      tile_step<Sh, 0, false>(w, lds, j, a);
-    else if (sl == 1)
-      tile_step<Sh, 1, false>(w, lds, j, a);
-    else
-      tile_step<Sh, 2, false>(w, lds, j, a);
-  }
+  for (; j < a.nT; ++j) tile_step_at<Sh, false>(w, lds, j, a);
   // P.V of the last computed half when it is the second half of the last tile (V_{nT-1}
   // landed at the last step's barrier and its slot was not refilled): half-step 2nT.
   if (a.nAct == 2 * a.nT) {
-    const int sl = (a.nT - 1) % kStages;
+    const int sl = (a.nT - 1) % Sh::kVSlots;
     if (sl == 0)
       pv_half<Sh, 0, 1>(w, lds);
     else if (sl == 1)
