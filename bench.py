@@ -163,7 +163,7 @@ def time_decode(dev, steps, warmup):
     o = torch.empty(B, H, D, device=dev, dtype=torch.bfloat16)
     lse = torch.empty(B, H, device=dev, dtype=torch.float32)
     ws_bytes = _C.decode_workspace_bytes(B, H, N)
-    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)  # counters start at zero
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
 

@@ -151,15 +151,12 @@ int tfgfa_fwd_bf16_strided(const void* q, const int64_t* q_strides,
  * cache_seqlens[b] + append > N_max) is only visible on the device: that batch
  * row gets NaN in O and LSE, and nothing is appended or read for it.
  *
- * workspace: device memory (16-byte aligned) for split-sequence partials and
- * per-head completion counters, or NULL.  It must be zero-filled before its
- * first use; every call leaves it zero-filled again, so it can be reused by
- * calls ordered on one stream (calls sharing a workspace must not overlap).
- * When B*H is below half the CU count the cache sequence is split over several
- * workgroups per head (up to what tfgfa_decode_workspace_bytes(B, H, N_max)
- * bytes hold), whose partials the last one to finish merges in the same
- * launch; with NULL (or too small for two splits) each head is one workgroup,
- * correct but slower for small B*H.
+ * workspace: device memory for split-sequence partials (16-byte aligned), or
+ * NULL.  The cache sequence is split over up to
+ * tfgfa_decode_workspace_bytes(B, H, N_max) / (B*H*260) workgroups per head,
+ * merged by a second kernel; with NULL (or too small for two splits) each head
+ * is one workgroup, correct but slower for small B*H.  Calls sharing a
+ * workspace must be ordered on one stream.
  */
 int tfgfa_decode_bf16(const void* q, const int64_t* q_strides,
                       void* k_cache, const int64_t* k_strides,

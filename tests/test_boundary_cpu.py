@@ -236,10 +236,9 @@ def test_c_abi_decode_validation(lib, kw, code):
 
 
 def test_decode_workspace_bytes(lib):
-    # Per-head counters padded to 256 B, then one partial (65 floats) per head per 128 rows.
-    assert lib.tfgfa_decode_workspace_bytes(8, 25, 1024) == 1024 + 8 * 25 * 8 * 65 * 4
-    assert lib.tfgfa_decode_workspace_bytes(1, 1, 1) == 256 + 65 * 4
-    assert lib.tfgfa_decode_workspace_bytes(1, 16, 8193) == 256 + 16 * 65 * 65 * 4
+    assert lib.tfgfa_decode_workspace_bytes(8, 25, 1024) == 8 * 25 * 8 * 65 * 4  # one slot per 128 rows
+    assert lib.tfgfa_decode_workspace_bytes(1, 1, 1) == 65 * 4
+    assert lib.tfgfa_decode_workspace_bytes(1, 16, 8193) == 16 * 65 * 65 * 4
     for bad in ((0, 1, 1), (1, 0, 1), (1, 1, 0), (-1, 2, 3)):
         assert lib.tfgfa_decode_workspace_bytes(*bad) == 0
     assert _C.decode_workspace_bytes(8, 25, 1024) == lib.tfgfa_decode_workspace_bytes(8, 25, 1024)

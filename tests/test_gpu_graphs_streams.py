@@ -87,7 +87,7 @@ def test_decode_steps_replay_from_a_graph():
     vns = [_randn((B, H, D), 60 + t) for t in range(steps)]
     q_in, kn_in, vn_in = (torch.empty_like(qs[0]) for _ in range(3))
     out = torch.empty(B, H, D, dtype=torch.bfloat16, device=DEV)
-    ws = torch.zeros(custom_flash_attn._C.decode_workspace_bytes(B, H, N_max), dtype=torch.uint8, device=DEV)
+    ws = torch.empty(custom_flash_attn._C.decode_workspace_bytes(B, H, N_max), dtype=torch.uint8, device=DEV)
     torch.cuda.synchronize()
 
     side = torch.cuda.Stream()

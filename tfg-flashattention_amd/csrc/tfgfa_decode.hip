@@ -28,10 +28,7 @@
 //   merged once at the end with the log-sum-exp rule
 //   o = sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i.
 //   S > 1: each workgroup writes its normalised partial (o_s, log2-domain lse_s) to the
-//   caller's workspace and takes a ticket from the head's counter (device-scope atomic after a
-//   release fence); the workgroup that draws the last ticket (acquire fence) combines the S
-//   partials, writes O and LSE and puts the counter back to zero.  One launch, no second
-//   kernel, and the workspace is left as it was found (zero counters) for the next call.
+//   caller's workspace and decode_merge_kernel combines the S partials of a head.
 //   S = 1: the workgroup writes O and LSE itself.
 //
 // Cache append: with k_new/v_new given, key L_b = cache_seqlens[b] is the new token: the
@@ -63,6 +60,7 @@ static_assert(kKeysPerLane % 2 == 0, "P.V pairs keys");
 constexpr int kWaveKeys = 16 * kKeysPerLane;   // keys per wave per block
 constexpr int kBlockKeys = kWaves * kWaveKeys; // keys per workgroup per block (chunk granule)
 constexpr int kGroups = 16;                    // key columns per wave (4 lanes each)
+constexpr int kMergeThreads = 256;             // decode_merge_kernel: one wave per head
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kPartFloats = kD + 1;            // per (head, split): o_s[64], lse_s
@@ -231,8 +229,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     const __bf16* __restrict__ Q, Vecs qs, __bf16* Kc, Rows ks, __bf16* Vc, Rows vs,
     const __bf16* __restrict__ Kn, Vecs kns, const __bf16* __restrict__ Vn, Vecs vns,
     const int* __restrict__ seqlens, __bf16* __restrict__ O, Vecs os, float* __restrict__ LSE,
-    unsigned* __restrict__ counters, float* __restrict__ part, int H, int N_max, int S, int C,
-    float scale_log2) {
+    float* __restrict__ part, int H, int N_max, int S, int C, float scale_log2) {
   constexpr int kStreams = kWaves * kGroups;       // softmax streams of the workgroup
   constexpr int kParts = kThreads / kD;            // first-level merge: streams in kParts parts
   constexpr int kPerPart = kStreams / kParts;
@@ -386,33 +383,37 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   if (S == 1) {
     store_o(O + b * os.b + h * os.h + d, on, valid);
     if (LSE != nullptr && d == 0) store_lse(LSE + bh, lse2 * kLn2, valid);
-    return;
+  } else {
+    float* pp = part + ((long long)bh * S + s) * kPartFloats;
+    pp[d] = on;
+    if (d == 0) pp[kD] = lse2;
   }
-  // S > 1 (one wave left, lane = head dim): publish this split's partial, then the head's last
-  // workgroup to arrive merges all S of them.
-  float* pp = part + ((long long)bh * S + s) * kPartFloats;
-  pp[d] = on;
-  if (d == 0) pp[kD] = lse2;
-  __threadfence();  // release: the partial is visible device-wide before the ticket
-  unsigned ticket = 0;
-  if (d == 0) ticket = atomicAdd(counters + bh, 1u);
-  ticket = __shfl(ticket, 0);
-  if (ticket != (unsigned)(S - 1)) return;
-  __threadfence();  // acquire: every other split's partial is visible
-  const float* ph = part + (long long)bh * S * kPartFloats;
-  float Mh = -INFINITY;
-  for (int i = 0; i < S; ++i) Mh = fmaxf(Mh, ph[i * kPartFloats + kD]);
-  const float Mh_use = (Mh == -INFINITY) ? 0.f : Mh;
-  float wt = 0.f, oh = 0.f;
-  for (int i = 0; i < S; ++i) {
-    const float w = exp2f(ph[i * kPartFloats + kD] - Mh_use);
+}
+
+// Combines the S partials of each head: one wave per head, lane = head dim.
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
+    const float* __restrict__ part, const int* __restrict__ seqlens, __bf16* __restrict__ O,
+    Vecs os, float* __restrict__ LSE, int BH, int H, int N_max, int S, bool append) {
+  const int bh = blockIdx.x * (kMergeThreads / 64) + (threadIdx.x >> 6);
+  if (bh >= BH) return;
+  const int d = threadIdx.x & 63;
+  const int b = bh / H, h = bh - b * H;
+  const int Lc = seqlens ? seqlens[b] : N_max;
+  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
+  const float* p = part + (long long)bh * S * kPartFloats;
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, p[s * kPartFloats + kD]);
+  const float M_use = (M == -INFINITY) ? 0.f : M;
+  float wt = 0.f, ot = 0.f;
+  for (int s = 0; s < S; ++s) {
+    const float w = exp2f(p[s * kPartFloats + kD] - M_use);
     wt += w;
-    oh = fmaf(w, ph[i * kPartFloats + d], oh);
+    ot = fmaf(w, p[s * kPartFloats + d], ot);
   }
-  store_o(O + b * os.b + h * os.h + d, wt > 0.f ? oh / wt : 0.f, valid);
+  const float on = wt > 0.f ? ot / wt : 0.f;
+  store_o(O + b * os.b + h * os.h + d, on, valid);
   if (LSE != nullptr && d == 0)
-    store_lse(LSE + bh, wt > 0.f ? (Mh + log2f(wt)) * kLn2 : -INFINITY, valid);
-  if (d == 0) counters[bh] = 0u;  // the next call on this workspace starts from zero
+    store_lse(LSE + bh, wt > 0.f ? (M + log2f(wt)) * kLn2 : -INFINITY, valid);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -420,11 +421,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
 
 // Splits for a cache of N_max rows.  One 8-wave workgroup per head keeps 128 KiB of K/V
 // loads in flight, enough to stream at HBM rate from one CU, so heads are not split while
-// B*H covers at least half the CUs (no partials, no merge kernel); below that, about one
-// workgroup per CU.  Chunks are a multiple of kBlockKeys, no split is empty.
+// B*H covers at least half the CUs (no partials, no merge kernel).  Below that, a head is
+// split into chunks of about kSplitKeys rows, at most about one workgroup per CU: a
+// workgroup has a fixed cost of several microseconds (the cache_seqlens load before the first
+// address, the first loads' latency, the stream merge), so a split of fewer rows loses more
+// than its extra parallelism gains (measured: 1 x 16 heads x 8192 rows takes 15.4 us with 4
+// or 8 splits per head, 19.9 us with 16, 30.1 us with 32).  Chunks are a multiple of
+// kBlockKeys, no split is empty.
+constexpr int kSplitKeys = 2048;
 static void choose_split(int BH, int N_max, int cu_count, int max_splits, int* S_out, int* C_out) {
   const int blocks = std::max(1, (N_max + kBlockKeys - 1) / kBlockKeys);
   int S = 2 * BH >= cu_count ? 1 : (cu_count + BH - 1) / BH;
+  S = std::min(S, (N_max + kSplitKeys - 1) / kSplitKeys);
   S = std::min(S, blocks);
   S = std::max(1, std::min(S, max_splits));
   const int C = (blocks + S - 1) / S * kBlockKeys;
@@ -474,10 +482,6 @@ static bool vecs_overlap(const Vecs& v, int B, int H) {
   return false;
 }
 
-// Workspace layout: one uint32 completion counter per head (zero between calls), padded to
-// 256 B, then the partials, B*H*S records of kPartFloats floats.
-static size_t counter_bytes(long long bh) { return ((size_t)bh * 4 + 255) & ~(size_t)255; }
-
 }  // namespace tfgfa_decode
 
 extern "C" size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max) {
@@ -486,8 +490,7 @@ extern "C" size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max) {
   // One partial per 128 cache rows: an upper bound on the splits of any block size >= 128,
   // so the size does not change with the kernel's tiling.
   const size_t blocks = ((size_t)N_max + kWorkspaceRows - 1) / kWorkspaceRows;
-  const long long bh = (long long)B * H;
-  return counter_bytes(bh) + (size_t)bh * blocks * kPartFloats * sizeof(float);
+  return (size_t)B * (size_t)H * blocks * kPartFloats * sizeof(float);
 }
 
 extern "C" int tfgfa_decode_bf16(const void* q, const int64_t* q_strides, void* k_cache,
@@ -534,10 +537,8 @@ extern "C" int tfgfa_decode_bf16(const void* q, const int64_t* q_strides, void* 
   const int st = tfgfa_device_info(&cu, nullptr, nullptr, 0);
   if (st != TFGFA_OK) return st;
   const size_t per_split = (size_t)bh * kPartFloats * sizeof(float);
-  const size_t cbytes = counter_bytes(bh);
-  const int ws_splits = workspace && workspace_bytes > cbytes
-                            ? (int)std::min((size_t)INT32_MAX, (workspace_bytes - cbytes) / per_split)
-                            : 0;
+  const int ws_splits =
+      workspace ? (int)std::min((size_t)INT32_MAX, workspace_bytes / per_split) : 0;
   int S, C;
   choose_split((int)bh, N_max, cu, std::max(1, ws_splits), &S, &C);
   if (bh * S > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
@@ -548,9 +549,18 @@ extern "C" int tfgfa_decode_bf16(const void* q, const int64_t* q_strides, void* 
                      static_cast<const __bf16*>(q), qs, static_cast<__bf16*>(k_cache), ks,
                      static_cast<__bf16*>(v_cache), vs, static_cast<const __bf16*>(k_new), kns,
                      static_cast<const __bf16*>(v_new), vns, cache_seqlens,
-                     static_cast<__bf16*>(o), os, lse, static_cast<unsigned*>(workspace),
-                     reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + cbytes), H,
-                     N_max, S, C, scale_log2);
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? TFGFA_OK : -(int)e;
+                     static_cast<__bf16*>(o), os, lse, static_cast<float*>(workspace), H, N_max,
+                     S, C, scale_log2);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return -(int)e;
+  if (S > 1) {
+    const int heads_per_wg = kMergeThreads / 64;
+    hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((bh + heads_per_wg - 1) / heads_per_wg)),
+                       dim3(kMergeThreads), 0, stream, static_cast<const float*>(workspace),
+                       cache_seqlens, static_cast<__bf16*>(o), os, lse, (int)bh, H, N_max, S,
+                       append);
+    e = hipGetLastError();
+    if (e != hipSuccess) return -(int)e;
+  }
+  return TFGFA_OK;
 }

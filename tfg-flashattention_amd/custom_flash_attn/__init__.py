@@ -238,10 +238,9 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     equals the last row of the causal forward over the first L tokens - what the reference's
     generate() recomputes from scratch for every token (src/py/model_inference.py:199-228).
     A length that does not fit the cache yields NaN for that batch row (checked on the device).
-    ``workspace``: optional uint8 device buffer for split-sequence partials and completion
-    counters, zero-filled before its first use (each call leaves it zeroed); when absent, a
-    zeroed buffer of ``_C.decode_workspace_bytes(B, H, N_max)`` bytes is kept per device and
-    stream and reused.
+    ``workspace``: optional uint8 device buffer for split-sequence partials (no initialisation
+    needed; an empty one runs each head as one workgroup); when absent, a buffer of
+    ``_C.decode_workspace_bytes(B, H, N_max)`` bytes is kept per device and stream and reused.
     """
     for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
         if not t.is_cuda:
@@ -302,12 +301,12 @@ _WORKSPACES: dict = {}
 
 
 def _decode_workspace(dev, nbytes: int) -> torch.Tensor:
-    """A zeroed decode workspace of at least ``nbytes`` for (device, current stream), reused
-    across calls: the kernel leaves it zeroed, and calls on one stream do not overlap."""
+    """A decode workspace of at least ``nbytes`` for (device, current stream), reused across
+    calls: it holds only the partials of one call, and calls on one stream do not overlap."""
     key = (dev, torch.cuda.current_stream(dev).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=dev)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
         _WORKSPACES[key] = ws
     return ws
 

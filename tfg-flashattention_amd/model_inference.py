@@ -176,8 +176,7 @@ class KVCache:
         self.seqlens = torch.zeros(batch, dtype=torch.int32, device=device)
         self.length = 0
         nbytes = custom_flash_attn._C.decode_workspace_bytes(batch, H, max_len)
-        # Split partials and completion counters; zeroed once, the kernel leaves it zeroed.
-        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
 
     def advance(self, n: int) -> None:
         self.length += n
