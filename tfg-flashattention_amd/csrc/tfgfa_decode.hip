@@ -15,9 +15,10 @@
 //
 // Work decomposition (split over the cache sequence)
 //   grid = B * H * S workgroups of 8 waves; workgroup (bh, s) covers keys [s*C, s*C + C) of
-//   head bh.  S = 1 while B*H covers at least half the CUs; below that S and C are chosen on
-//   the host so the grid fills the chip.  Inside a workgroup, wave w takes 32-key blocks
-//   w, w+8, w+16, ... of the chunk.
+//   head bh.  S = 1 while B*H covers at least half the CUs; below that the host splits each
+//   head into chunks of about 2048 keys (at most about one workgroup per CU; a workgroup's
+//   fixed cost outweighs the parallelism of shorter chunks).  Inside a workgroup, wave w
+//   takes 32-key blocks w, w+8, w+16, ... of the chunk.
 //   Lane l of a wave handles keys (block + l/4) and (block + l/4 + 16), head dims 8c .. 8c+7
 //   and 32+8c .. 32+8c+7 (c = l%4): two buffer_load_dwordx4 per key row per lane, so a wave
 //   instruction reads 16 rows x 64 contiguous bytes.  The next block's K and V loads are
