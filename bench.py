@@ -13,7 +13,7 @@ Prints one JSON line.  ``value`` is TFLOP/s with the FlashAttention causal conve
 src/py/model_inference.py:68-75) on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 2000] [--no-cpu-baseline] [--no-strided]
-                      [--no-decode]
+                      [--no-decode] [--no-generate]
 """
 import argparse
 import json
@@ -86,11 +86,82 @@ def cpu_baseline(gpu_o_sample, q_sample, k_sample, v_sample, heads_in_sample):
         "cores": cores,
         "kind": "port",
         "sample": (f"{heads_in_sample} of {B * H} (batch, head) pairs, N={N}, d={D}, of bench input "
-                   f"set 0; torch {torch.__version__} fp32 manual path on {cores} threads, median of "
-                   f"3 runs = {sec:.3f} s; TFLOP/s on the same algorithmic FLOP count as the GPU"),
+                   f"set 0; torch {torch.__version__} fp32 manual path on {cores} threads of "
+                   f"{cpu_model()}, median of 3 runs = {sec:.3f} s; TFLOP/s on the same algorithmic "
+                   f"FLOP count as the GPU"),
         "seconds_per_sample": sec,
         "max_abs_diff_vs_gpu": max_err,
     }
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+GEN_MODEL, GEN_PROMPT, GEN_NEW = "gpt2-medium (355M)", 48, 20
+
+
+def time_generate(dev, runs=5, warmup=2):
+    """The reference's own benchmark (src/py/model_inference.py:444-457): generate() of 20 new
+    tokens after a prompt, temperature 1.0, no top-k, B = 1, timed with events around the whole
+    call.  GPT-2-medium with seeded random weights (no checkpoint download) and a prompt of 48
+    random token ids (the reference's prompt is text, tokenised by tiktoken, not available).
+    Four ways: the reference's loop (the whole prefix re-run per token) with its torch
+    "manual" attention, the same loop with this build's forward kernel ("hip"), the cached loop
+    (one prefill, then the decode kernel per token), and the cached loop with each decode step
+    replayed from a HIP graph (captured once, before the timing)."""
+    import torch
+
+    import model_inference as mi
+
+    torch.manual_seed(0)
+    model = mi.GPTModel(mi.gpt2_config(GEN_MODEL, "hip")).eval()
+    mi.init_gpt2_weights(model, 5)
+    model = model.to(dev)
+    prompt = torch.randint(0, 50257, (1, GEN_PROMPT), generator=torch.Generator().manual_seed(9)).to(dev)
+
+    def set_impl(impl):
+        for blk in model.trf_blocks:
+            blk.att.impl_type = impl
+
+    set_impl("hip")
+    decoder = mi.GraphedDecoder(model, 1, GEN_PROMPT + GEN_NEW, dev)  # capture: once, untimed
+
+    def graphed(m, idx, n, ctx):
+        return mi.generate_graphed(m, idx, n, ctx, decoder=decoder)
+
+    out = {}
+    for label, impl, fn in (("reference_loop_manual_attention", "manual", mi.generate),
+                            ("reference_loop_hip_forward", "hip", mi.generate),
+                            ("cached_hip_decode", "hip", mi.generate_cached),
+                            ("cached_hip_decode_graph", "hip", graphed)):
+        set_impl(impl)
+        times = []
+        for r in range(warmup + runs):
+            torch.manual_seed(123 + r)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            ids = fn(model, prompt, GEN_NEW, 1024)
+            e1.record()
+            torch.cuda.synchronize()
+            assert ids.shape == (1, GEN_PROMPT + GEN_NEW)
+            if r >= warmup:
+                times.append(e0.elapsed_time(e1))
+        ms = statistics.median(times)
+        out[label] = {"ms_per_call": round(ms, 3), "tokens_per_s": round(GEN_NEW / (ms * 1e-3), 1)}
+    set_impl("hip")
+    del model, decoder
+    torch.cuda.empty_cache()
+    out["workload"] = (f"{GEN_MODEL}, random weights, B=1, prompt {GEN_PROMPT} random ids, {GEN_NEW} new "
+                       f"tokens, temperature 1.0; median of {runs} calls after {warmup}")
+    return out
 
 
 def time_strided_views(dev, steps, warmup):
@@ -239,6 +310,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the decode-step leg (KV-cache attention, HBM-bound)")
+    ap.add_argument("--no-generate", action="store_true",
+                    help="skip the token-generation leg (the reference's generate() benchmark)")
     ap.add_argument("--no-strided", action="store_true",
                     help="skip the second timing of the same workload on strided (B, N, H, 64) views")
     ap.add_argument("--cpu-heads", type=int, default=200,
@@ -344,6 +417,8 @@ def main():
         result["strided_gpt2_views"] = time_strided_views(dev, max(1, args.steps // 2), max(1, args.warmup // 2))
     if not args.no_decode:
         result["decode"] = time_decode(dev, args.steps, args.warmup)
+    if not args.no_generate:
+        result["generate"] = time_generate(dev)
     if not args.no_cpu_baseline:
         nh = max(1, min(args.cpu_heads, B * H))
         q, k, v, o = (t.reshape(1, B * H, N, D)[:, :nh] for t in sets[0][:4])

@@ -133,3 +133,36 @@ def test_top_k_filter_keeps_k_tokens_per_row():
         nxt = mi._next_token(logits, 1.0, 2)
         assert nxt[0, 0].item() in (1, 3) and nxt[1, 0].item() in (0, 2)
     assert mi._next_token(logits, 0.0, 2).flatten().tolist() == [1, 0]
+
+
+@pytest.mark.gpu
+def test_graphed_decode_steps_match_eager_cached_steps():
+    """Decode steps replayed from a HIP graph give the eager cached steps' logits bitwise, step
+    after step, with eager work on the stream between replays; greedy generation through the
+    graph equals greedy generate_cached."""
+    torch.manual_seed(0)
+    cfg = _small_cfg("hip")
+    model = mi.GPTModel(cfg).eval().to("cuda:0")
+    mi.init_gpt2_weights(model, SEED_W)
+    B, P, T = 2, 13, 9
+    seq = torch.randint(0, cfg["vocab_size"], (B, P + T), generator=torch.Generator().manual_seed(8)).to("cuda:0")
+    cfg_c = {"n_heads": 8, "emb_dim": 512, "n_layers": 4}
+    eager_cache = mi.KVCache(cfg_c, B, P + T, "cuda:0")
+    dec = mi.GraphedDecoder(model, B, P + T, "cuda:0")
+    with torch.no_grad():
+        le = model(seq[:, :P], kv_cache=eager_cache)[:, -1].float()
+        lg = dec.prefill(seq[:, :P]).float()
+        assert torch.equal(le, lg)
+        for t in range(P, P + T):
+            le = model(seq[:, t:t + 1], kv_cache=eager_cache)[:, -1].float()
+            _ = (torch.randn(64, 64, device="cuda:0") @ torch.randn(64, 64, device="cuda:0")).sum()
+            lg = dec.step(seq[:, t:t + 1]).float()
+            torch.cuda.synchronize()
+            _say(f"graphed decode step {t}: max|d logits| = {(le - lg).abs().max().item():.3e}")
+            assert torch.equal(le, lg), f"step {t}: graph replay differs from the eager step"
+    assert dec.cache.length == P + T and torch.equal(dec.cache.seqlens.cpu(), torch.full((B,), P + T, dtype=torch.int32))
+    idx = seq[:, :P]
+    a = mi.generate_cached(model, idx, 8, 256, temperature=0.0)
+    b = mi.generate_graphed(model, idx, 8, 256, temperature=0.0, decoder=dec)
+    c = mi.generate_graphed(model, idx, 8, 256, temperature=0.0)
+    assert torch.equal(a, b) and torch.equal(a, c)

@@ -182,6 +182,54 @@ class KVCache:
         self.length += n
         self.seqlens.add_(n)
 
+    def reset(self) -> None:
+        self.length = 0
+        self.seqlens.zero_()
+
+
+class GraphedDecoder:
+    """One decode step of ``model`` (batch ``batch``, cache of ``max_len`` rows) captured in a
+    HIP graph and replayed per token, so a step costs one graph launch instead of the ~20
+    kernel launches (and their Python) per layer of an eager step.
+
+    The step reads its token from ``self.tok`` and leaves the last position's logits in
+    ``self.logits``.  Everything it depends on lives in device memory: the positions and the
+    decode kernel's lengths come from ``cache.seqlens``, which the graph itself advances.
+    Capture runs two eager warm-up steps on a side stream first (they write cache rows 0-1,
+    which the prefill later overwrites), then resets the cache."""
+
+    def __init__(self, model, batch: int, max_len: int, device):
+        cfg = {"n_heads": model.trf_blocks[0].att.num_heads, "emb_dim": model.tok_emb.embedding_dim,
+               "n_layers": len(model.trf_blocks)}
+        self.model = model
+        self.cache = KVCache(cfg, batch, max_len, device)
+        self.tok = torch.zeros(batch, 1, dtype=torch.long, device=device)
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.no_grad(), torch.cuda.stream(side):
+            self.cache.length = 1
+            self.cache.seqlens.fill_(1)
+            for _ in range(2):
+                model(self.tok, kv_cache=self.cache)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, stream=side):
+                self.logits = model(self.tok, kv_cache=self.cache)[:, -1, :]
+        torch.cuda.current_stream(device).wait_stream(side)
+        self.cache.reset()
+
+    def prefill(self, idx):
+        """Eager prefill of the prompt; returns the last position's logits."""
+        with torch.no_grad():
+            return self.model(idx, kv_cache=self.cache)[:, -1, :]
+
+    def step(self, tok):
+        """Appends ``tok`` ((B, 1) token ids) and returns the next logits (a view of the
+        graph's output buffer, overwritten by the next step)."""
+        self.tok.copy_(tok)
+        self.graph.replay()
+        self.cache.length += 1  # the graph advanced cache.seqlens on the device
+        return self.logits
+
 
 class LayerNorm(nn.Module):
     """LayerNorm with eps 1e-5 and biased variance (model_inference.py:96-107)."""
@@ -266,11 +314,15 @@ class GPTModel(nn.Module):
 
     def forward(self, in_idx, kv_cache=None):
         """Logits for ``in_idx``.  With ``kv_cache`` the tokens continue the cached sequence:
-        positions start at ``kv_cache.length`` and the cache advances by the token count."""
+        positions start at the cached length, read from ``kv_cache.seqlens`` on the device (so a
+        captured decode step stays correct on replay), and the cache advances by the token
+        count."""
         _, seq_len = in_idx.shape
-        start = 0 if kv_cache is None else kv_cache.length
         tok_embeds = self.tok_emb(in_idx)
-        pos_embeds = self.pos_emb(torch.arange(start, start + seq_len, device=in_idx.device))
+        pos = torch.arange(seq_len, device=in_idx.device)
+        if kv_cache is not None:
+            pos = kv_cache.seqlens[:, None].long() + pos  # (B, T)
+        pos_embeds = self.pos_emb(pos)
         x = self.drop_emb(tok_embeds + pos_embeds)
         if kv_cache is None:
             x = self.trf_blocks(x)
@@ -332,6 +384,29 @@ def generate_cached(model, idx, max_new_tokens, context_size, temperature=1.0, t
             break
         idx = torch.cat((idx, idx_next), dim=1)
         step_in = idx_next
+    return idx
+
+
+def generate_graphed(model, idx, max_new_tokens, context_size, temperature=1.0, top_k=None,
+                     eos_id=None, decoder: GraphedDecoder | None = None):
+    """:func:`generate_cached` with every decode step replayed from a :class:`GraphedDecoder`
+    (built here unless one for this batch and length is passed in).  Same sampling."""
+    if idx.shape[1] + max_new_tokens > context_size:
+        raise ValueError(f"prompt ({idx.shape[1]}) + max_new_tokens ({max_new_tokens}) exceeds "
+                         f"context_size ({context_size})")
+    if decoder is None:
+        decoder = GraphedDecoder(model, idx.shape[0], idx.shape[1] + max_new_tokens, idx.device)
+    elif decoder.cache.max_len < idx.shape[1] + max_new_tokens:
+        raise ValueError("the decoder's cache is shorter than prompt + max_new_tokens")
+    decoder.cache.reset()
+    logits = decoder.prefill(idx)
+    for i in range(max_new_tokens):
+        idx_next = _next_token(logits, temperature, top_k)
+        if idx_next == eos_id:
+            break
+        idx = torch.cat((idx, idx_next), dim=1)
+        if i + 1 < max_new_tokens:
+            logits = decoder.step(idx_next)
     return idx
 
 
