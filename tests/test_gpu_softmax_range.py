@@ -1,0 +1,83 @@
+"""The forward's softmax over extreme score patterns (GPU box only).
+
+The kernel keeps a per-row exp2 offset that moves only when a score passes it by a margin (64
+log2 units for bf16, 15 for fp16); a move rescales O and both sums and recomputes the half's
+probabilities.  Random inputs at the configs' scales move it about once per row, so these
+cases force the other paths: scores that climb by far more than the margin every half (a move
+on every half, with rescale factors that underflow to 0), scores that fall (no move after the
+first half), halves that alternate high and low, and scores of magnitude ~1e4 (one-hot rows).
+
+Oracle: attention_np (fp64, tests/test_oracle.py) on the same bf16/fp16-rounded inputs.
+Tolerances as everywhere: max|dO| <= 2e-2, mean|dO| <= 2e-3; LSE within 1e-3 plus the fp32
+rounding of an LSE of that magnitude (4e-7 relative; it matters only for the ~1e4 case).
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_np
+
+import custom_flash_attn
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _case(kind, N, D, seed, dtype):
+    """q, k, v float32 arrays (1, 2, N, D) holding dtype-representable values."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    q = g.standard_normal((1, 2, N, D), dtype=np.float32) * 0.1
+    k = g.standard_normal((1, 2, N, D), dtype=np.float32) * 0.1
+    v = g.standard_normal((1, 2, N, D), dtype=np.float32)
+    j = np.arange(N, dtype=np.float32)
+    # With q[..., 0] = 8, adding c to k[..., 0] adds 8 * c / sqrt(D) to the score (natural log
+    # units); unit(A) is the c that adds A.
+    unit = lambda a: a * math.sqrt(D) / 8.0
+    if kind == "rising":      # +0.75 per key (~35 log2 units per 32-key half)
+        q[..., 0] = 8.0
+        k[..., 0] += unit(0.75) * j
+    elif kind == "falling":   # the first keys dominate; later probabilities underflow
+        q[..., 0] = 8.0
+        k[..., 0] += unit(0.75) * (N - j)
+    elif kind == "zigzag":    # 32-key halves alternately +40 and -40
+        q[..., 0] = 8.0
+        k[..., 0] += unit(40.0) * np.where((j // 32) % 2 == 0, 1.0, -1.0)
+    elif kind == "huge":      # scores of order 1e3: one-hot rows
+        q *= 3000.0
+        k *= 30.0
+    t = DTYPES[dtype]
+    rnd = lambda x: torch.from_numpy(x).to(t).float().numpy()
+    return rnd(q), rnd(k), rnd(v)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("kind", ["rising", "falling", "zigzag", "huge"])
+@pytest.mark.parametrize("N,D", [(300, 64), (1024, 64), (700, 128)])
+def test_extreme_score_patterns(kind, N, D, dtype):
+    q, k, v = _case(kind, N, D, 17 * N + D, dtype)
+    t = DTYPES[dtype]
+    qd, kd, vd = (torch.from_numpy(x).to(t).to(DEV) for x in (q, k, v))
+    scale = 1.0 / math.sqrt(D)
+    o, lse = custom_flash_attn.attention(qd, kd, vd, return_lse=True)
+    torch.cuda.synchronize()
+    o_ref, l_ref = attention_np(q, k, v, scale, True)
+    o = o.float().cpu().numpy().astype(np.float64)
+    lse = lse.cpu().numpy().astype(np.float64)
+    d = np.abs(o - o_ref)
+    dl = np.abs(lse - l_ref)
+    span = np.abs(l_ref).max()
+    _say(f"{kind} {dtype} N={N} D={D}: |LSE| up to {span:.1f}; max|dO|={d.max():.3e} "
+         f"mean|dO|={d.mean():.3e} max|dLSE|={dl.max():.3e}")
+    assert np.isfinite(o).all() and np.isfinite(lse).all(), "non-finite output"
+    assert d.max() <= 2e-2 and d.mean() <= 2e-3
+    assert (dl <= 1e-3 + 4e-7 * np.abs(l_ref)).all()
