@@ -40,13 +40,13 @@
 extern "C" {
 #endif
 
-#define TFGFA_ABI_VERSION 4
+#define TFGFA_ABI_VERSION 5
 
 /* Status codes (> 0: invalid argument). */
 #define TFGFA_OK                 0
 #define TFGFA_ERR_NULL_POINTER   1  /* q, k, v or o is NULL                          */
 #define TFGFA_ERR_BAD_SHAPE      2  /* B, H or N negative                            */
-#define TFGFA_ERR_HEAD_DIM       3  /* D not a multiple of 8 in [8, 128] (fwd), not 64 (decode) */
+#define TFGFA_ERR_HEAD_DIM       3  /* D not a multiple of 8 in [8, 128] (not 64: *_bf16 entries) */
 #define TFGFA_ERR_SCALE          4  /* softmax_scale not finite or not > 0           */
 #define TFGFA_ERR_CAUSAL_FLAG    5  /* causal is neither 0 nor 1                     */
 #define TFGFA_ERR_TOO_LARGE      6  /* grid or element count exceeds the limits      */
@@ -174,6 +174,37 @@ int tfgfa_decode_bf16(const void* q, const int64_t* q_strides,
  * device.  No counterpart in the reference.
  */
 size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max);
+
+/*
+ * tfgfa_decode_bf16 widened to the element types and head dims of tfgfa_fwd:
+ * dtype TFGFA_DTYPE_BF16 or TFGFA_DTYPE_F16 for q, the caches, k_new, v_new and
+ * o (fp32 softmax either way), D a multiple of 8 in [8, 128] (the cache row
+ * stride n >= D).  Everything else - operands, lengths, append, NaN for
+ * invalid lengths, workspace - as tfgfa_decode_bf16, with the workspace split
+ * count bounded by tfgfa_decode_workspace_size(B, H, N_max, D) /
+ * (B*H*(D+1)*4).  With dtype TFGFA_DTYPE_BF16 and D = 64 the results are
+ * bitwise those of tfgfa_decode_bf16.  Replaces, as tfgfa_decode_bf16 does,
+ * the per-token full forward of generate() (src/py/model_inference.py:199-228),
+ * for the fp16 / d <= 128 surface of the Triton wrapper
+ * (src/py/triton_implementation.py:184-197).
+ */
+int tfgfa_decode(const void* q, const int64_t* q_strides,
+                 void* k_cache, const int64_t* k_strides,
+                 void* v_cache, const int64_t* v_strides,
+                 const void* k_new, const int64_t* k_new_strides,
+                 const void* v_new, const int64_t* v_new_strides,
+                 const int* cache_seqlens,
+                 void* o, const int64_t* o_strides, float* lse,
+                 int B, int H, int N_max, int D, int dtype, float softmax_scale,
+                 void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/*
+ * Workspace bytes that let tfgfa_decode use every split it may choose for head
+ * dim D (0 when B, H or N_max is not positive or D is not a multiple of 8 in
+ * [8, 128]).  tfgfa_decode_workspace_bytes(B, H, N_max) equals this with
+ * D = 64.  No counterpart in the reference.
+ */
+size_t tfgfa_decode_workspace_size(int B, int H, int N_max, int D);
 
 /*
  * Human-readable text for a status code returned by any tfgfa_* function.

@@ -42,6 +42,12 @@ def lib():
         ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.tfgfa_decode_workspace_bytes.restype = ctypes.c_size_t
     lib.tfgfa_decode_workspace_bytes.argtypes = [ctypes.c_int] * 3
+    lib.tfgfa_decode.restype = ctypes.c_int
+    lib.tfgfa_decode.argtypes = [ctypes.c_void_p, ctypes.c_void_p] * 5 + [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 5 + [
+        ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.tfgfa_decode_workspace_size.restype = ctypes.c_size_t
+    lib.tfgfa_decode_workspace_size.argtypes = [ctypes.c_int] * 4
     lib.tfgfa_fwd.restype = ctypes.c_int
     lib.tfgfa_fwd.argtypes = [ctypes.c_void_p, ctypes.c_void_p] * 4 + [ctypes.c_void_p] + [
         ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
@@ -53,7 +59,8 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     names = _header_functions()
-    assert names == ["tfgfa_abi_version", "tfgfa_decode_bf16", "tfgfa_decode_workspace_bytes",
+    assert names == ["tfgfa_abi_version", "tfgfa_decode", "tfgfa_decode_bf16",
+                     "tfgfa_decode_workspace_bytes", "tfgfa_decode_workspace_size",
                      "tfgfa_device_info", "tfgfa_fwd", "tfgfa_fwd_bf16", "tfgfa_fwd_bf16_strided",
                      "tfgfa_strerror"]
     for n in names:
@@ -233,6 +240,69 @@ def _decode_args(B=2, H=3, N=100, q=None, kc=None, vc=None, kn=None, vn=None, se
 ])
 def test_c_abi_decode_validation(lib, kw, code):
     assert lib.tfgfa_decode_bf16(*_decode_args(**kw)) == _header_define(code)
+
+
+def _general(args, dtype=0):
+    """tfgfa_decode_bf16 arguments -> tfgfa_decode arguments (dtype after D)."""
+    return args[:18] + (dtype,) + args[18:]
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(), "TFGFA_ERR_NULL_POINTER"),                          # bf16 D = 64, q NULL
+    (dict(B=-1), "TFGFA_ERR_BAD_SHAPE"),
+    (dict(D=128, ks=_st(3 * 100 * 128, 100 * 128, 128, 1), vs=_st(3 * 100 * 128, 100 * 128, 128, 1),
+          qs=_s3(384, 128, 1), os_=_s3(384, 128, 1)), "TFGFA_ERR_NULL_POINTER"),   # D = 128 accepted
+    (dict(D=40), "TFGFA_ERR_NULL_POINTER"),                      # rows of 64 >= 40: accepted
+    (dict(D=8), "TFGFA_ERR_NULL_POINTER"),
+    (dict(D=36), "TFGFA_ERR_HEAD_DIM"),                          # not a multiple of 8
+    (dict(D=0), "TFGFA_ERR_HEAD_DIM"),
+    (dict(D=136), "TFGFA_ERR_HEAD_DIM"),                         # > 128
+    (dict(D=128), "TFGFA_ERR_STRIDE"),                           # cache rows of 64 < D
+    (dict(D=72, os_=_s3(72, 64, 1), qs=_s3(216, 72, 1),
+          ks=_st(3 * 100 * 72, 100 * 72, 72, 1), vs=_st(3 * 100 * 72, 100 * 72, 72, 1)),
+     "TFGFA_ERR_STRIDE"),                                        # O rows of 72 at stride 64 overlap
+    (dict(scale=-1.0), "TFGFA_ERR_SCALE"),
+    (dict(kn=P, vn=P), "TFGFA_ERR_CACHE"),
+])
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_c_abi_general_decode_validation(lib, kw, code, dtype):
+    assert lib.tfgfa_decode(*_general(_decode_args(**kw), dtype)) == _header_define(code)
+
+
+@pytest.mark.parametrize("dtype", [2, -1, 100])
+def test_c_abi_general_decode_rejects_unknown_dtype(lib, dtype):
+    assert lib.tfgfa_decode(*_general(_decode_args(), dtype)) == _header_define("TFGFA_ERR_DTYPE")
+
+
+def test_general_decode_agrees_with_bf16_entry_on_d64_validation(lib):
+    """Every argument case of the bf16 entry gets the same status from tfgfa_decode with
+    dtype bf16, except head dims the general entry takes."""
+    for kw in (dict(B=-1), dict(N=-5), dict(scale=0.0), dict(kn=P), dict(kn=P, vn=P), dict(B=0),
+               dict(), dict(qs=_s3(192, 64, 2)), dict(ks=_st(3 * 100 * 64, 100 * 64, 32, 1)),
+               dict(os_=_s3(64, 64, 1)), dict(N=1 << 24), dict(q=P + 8, kc=P, vc=P, o=P),
+               dict(q=P, kc=P, vc=P, o=P, ws=P + 8, ws_bytes=4096)):
+        args = _decode_args(**kw)
+        assert lib.tfgfa_decode(*_general(args)) == lib.tfgfa_decode_bf16(*args), kw
+
+
+def test_decode_workspace_size(lib):
+    assert lib.tfgfa_decode_workspace_size(8, 25, 1024, 64) == lib.tfgfa_decode_workspace_bytes(8, 25, 1024)
+    assert lib.tfgfa_decode_workspace_size(1, 1, 1, 128) == 129 * 4
+    assert lib.tfgfa_decode_workspace_size(2, 3, 300, 40) == 6 * 3 * 41 * 4
+    for bad in ((0, 1, 1, 64), (1, 0, 1, 64), (1, 1, 0, 64), (1, 1, 1, 0), (1, 1, 1, 12),
+                (1, 1, 1, 136)):
+        assert lib.tfgfa_decode_workspace_size(*bad) == 0
+    assert _C.decode_workspace_size(2, 3, 300, 40) == lib.tfgfa_decode_workspace_size(2, 3, 300, 40)
+
+
+def test_pybind_general_decode_raises_runtime_error_with_message():
+    z3 = (0, 0, 0)
+    with pytest.raises(RuntimeError, match="tfgfa_decode failed .*dtype"):
+        _C.decode_general(P, z3, P, (0, 0, 0, 1), P, (0, 0, 0, 1), 0, z3, 0, z3, 0, P, z3, 0,
+                          2, 3, 100, 64, 7, 0.125, 0, 0, 0)
+    with pytest.raises(RuntimeError, match="unsupported head dimension"):
+        _C.decode_general(P, z3, P, (0, 0, 0, 1), P, (0, 0, 0, 1), 0, z3, 0, z3, 0, P, z3, 0,
+                          2, 3, 100, 20, 1, 0.125, 0, 0, 0)
 
 
 def test_decode_workspace_bytes(lib):

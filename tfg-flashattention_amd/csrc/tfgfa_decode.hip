@@ -1,4 +1,5 @@
-// tfgfa_decode.hip - one decode step of attention over a KV cache, MI355X (gfx950), bf16.
+// tfgfa_decode.hip - one decode step of attention over a KV cache, MI355X (gfx950), bf16 or
+// fp16, head dim a multiple of 8 up to 128.
 //
 // What it replaces: the reference's generate() has no KV cache; every new token re-runs the
 // whole prefix through the model, i.e. a full causal forward of which only the last query row
@@ -8,27 +9,28 @@
 // (the same math as model_inference.py:68-75 restricted to row L-1).  This file computes that
 // row directly from a cache, optionally appending the new token's k/v first.
 //
-// Bound: HBM.  Every cached K and V byte is read once (2 * 128 B per key per head) and the
-// arithmetic is 2 * 64 MACs per key, about 0.5 FLOP/B, so the MFMA units have nothing to do:
-// scores and the P.V update are VALU v_dot2_f32_bf16 on the bf16 values as loaded (two MACs
+// Bound: HBM.  Every cached K and V byte is read once (4D bytes per key per head) and the
+// arithmetic is 2D MACs per key, about 0.5 FLOP/B, so the MFMA units have nothing to do:
+// scores and the P.V update are VALU v_dot2_f32_{bf16,f16} on the values as loaded (two MACs
 // per instruction, fp32 accumulate), which keeps the VALU time per byte below the HBM time.
 //
 // Work decomposition (split over the cache sequence)
 //   grid = B * H * S workgroups of 8 waves; workgroup (bh, s) covers keys [s*C, s*C + C) of
 //   head bh.  S = 1 while B*H covers at least half the CUs; below that the host splits each
-//   head into chunks of about 2048 keys (at most about one workgroup per CU; a workgroup's
-//   fixed cost outweighs the parallelism of shorter chunks).  Inside a workgroup, wave w
-//   takes 32-key blocks w, w+8, w+16, ... of the chunk.
-//   Lane l of a wave handles keys (block + l/4) and (block + l/4 + 16), head dims 8c .. 8c+7
-//   and 32+8c .. 32+8c+7 (c = l%4): two buffer_load_dwordx4 per key row per lane, so a wave
-//   instruction reads 16 rows x 64 contiguous bytes.  The next block's K and V loads are
-//   issued before the current block is computed.
+//   head so that the workgroups fill one round of workgroup slots (choose_split).  Inside a
+//   workgroup, wave w takes 32-key blocks w, w+8, w+16, ... of the chunk.
+//   Lane l of a wave handles keys (block + l/4) and (block + l/4 + 16) and, for each 32-dim
+//   piece p of the row, head dims 32p + 8c .. 32p + 8c + 7 (c = l%4): one buffer_load_dwordx4
+//   per piece per key row per lane, so a wave instruction reads 16 rows x 64 contiguous bytes.
+//   Pieces at or past the head dim load from an out-of-range offset (zeros, no memory access)
+//   and are never stored.  The next block's K and V loads are issued before the current
+//   block is computed.
 //   Each quad of lanes (one key column of the wave) runs its own online softmax over its
 //   keys, so the only cross-lane step per block is the 2-step DPP sum of a dot product within
 //   the quad; the 128 streams of a workgroup (in LDS) and, when S > 1, the workgroups are
 //   merged once at the end with the log-sum-exp rule
 //   o = sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i.
-//   S > 1: each workgroup writes its normalised partial (o_s, log2-domain lse_s) to the
+//   S > 1: each workgroup writes its normalised partial (o_s[D], log2-domain lse_s) to the
 //   caller's workspace and decode_merge_kernel combines the S partials of a head.
 //   S = 1: the workgroup writes O and LSE itself.
 //
@@ -51,9 +53,10 @@
 
 #include "tfgfa.h"
 
-namespace tfgfa_decode {
+namespace tfgfa_dec {
 
-constexpr int kD = 64;
+constexpr int kD = 64;                         // head dim of tfgfa_decode_bf16
+constexpr int kMaxD = 128;                     // largest head dim of tfgfa_decode
 constexpr int kThreads = 512;
 constexpr int kWaves = 8;
 constexpr int kKeysPerLane = 2;                // keys per lane per block (rows 16 apart)
@@ -64,43 +67,83 @@ constexpr int kGroups = 16;                    // key columns per wave (4 lanes 
 constexpr int kMergeThreads = 256;             // decode_merge_kernel: one wave per head
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kPartFloats = kD + 1;            // per (head, split): o_s[64], lse_s
 constexpr int kWorkspaceRows = 128;            // cache rows per split counted by the workspace
 static_assert(kBlockKeys % kWorkspaceRows == 0, "splits must not outnumber workspace slots");
 // A buffer offset past any num_records this file builds (those stay below 2^31 - 2^24): the
-// load returns zero without a memory access.  Used for the prefetch after the last block.
-constexpr int kOutOfRange = 0x7FFFFFF0;
+// load returns zero without a memory access.  Used for the prefetch after the last block and
+// for the pieces of a row past the head dim.
+constexpr uint32_t kOutOfRange = 0x7FFFFFF0u;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-struct Rows {  // element strides of a (B, H, N, 64) operand (last dim dense)
+struct Rows {  // element strides of a (B, H, N, D) operand (last dim dense)
   long long b, h, n;
 };
-struct Vecs {  // element strides of a (B, H, 64) operand
+struct Vecs {  // element strides of a (B, H, D) operand
   long long b, h;
+};
+
+// Element type: the pair dot product v_dot2_f32_{bf16,f16} (a.lo*b.lo + a.hi*b.hi + c, fp32
+// accumulate; products of two bf16 or two fp16 values are exact in fp32), the halves of a
+// 32-bit pair as fp32, and the quiet-NaN pattern.
+template <class T>
+struct DElem;
+template <>
+struct DElem<__bf16> {
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, b), c, false);
+  }
+  static __device__ __forceinline__ float lo(uint32_t x) { return __uint_as_float(x << 16); }
+  static __device__ __forceinline__ float hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+  static constexpr unsigned short kNaN = 0x7FC0;
+};
+template <>
+struct DElem<_Float16> {
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
+                                  false);
+  }
+  static __device__ __forceinline__ float lo(uint32_t x) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(x & 0xffffu));
+  }
+  static __device__ __forceinline__ float hi(uint32_t x) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(x >> 16));
+  }
+  static constexpr unsigned short kNaN = 0x7E00;
+};
+
+// Compile-time shape: element type T; kDP pieces of 32 head dims per key row (a lane holds
+// 8 dims of each piece); kMaskD: the head dim D may be below 32 * kDP (a multiple of 8), and
+// the 16-byte pieces at dims >= D are neither read nor written.
+template <class T_, int kDP_, bool kMaskD_>
+struct DShape {
+  typedef T_ T;
+  static constexpr int kDP = kDP_;
+  static constexpr int kDm = 32 * kDP_;
+  static constexpr bool kMaskD = kMaskD_;
 };
 
 // NaN marks results of invalid cache lengths.  The device pass is compiled with
 // -fno-honor-nans, under which a floating-point select may drop a NaN operand, so these
 // stores choose between bit patterns and write them through integer pointers.
-__device__ __forceinline__ void store_o(__bf16* p, float v, bool valid) {
-  const unsigned short bits = __builtin_bit_cast(unsigned short, (__bf16)v);
-  *reinterpret_cast<unsigned short*>(p) = valid ? bits : (unsigned short)0x7FC0;
+template <class T>
+__device__ __forceinline__ void store_o(T* p, float v, bool valid) {
+  const unsigned short bits = __builtin_bit_cast(unsigned short, (T)v);
+  *reinterpret_cast<unsigned short*>(p) = valid ? bits : DElem<T>::kNaN;
 }
 __device__ __forceinline__ void store_lse(float* p, float v, bool valid) {
   *reinterpret_cast<uint32_t*>(p) = valid ? __float_as_uint(v) : 0x7FC00000u;
 }
 
-__device__ __forceinline__ float bf_lo(uint32_t x) { return __uint_as_float(x << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int nbytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, nbytes, 0x00020000);
 }
 
-__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
 // Sum over the 4 lanes of a key column (one quad): xor 1 and xor 2 by DPP quad permutations.
@@ -110,37 +153,40 @@ __device__ __forceinline__ float quad_sum(float x) {
   return x;
 }
 
-// This lane's share of one block of a wave: keys key0 + 16r (r < kKeysPerLane), each as two
-// 16-byte pieces: dims 8c .. 8c+7 (piece 0, bytes 16c) and 32+8c .. +7 (piece 1, bytes
-// 64+16c).  A wave instruction reads 16 rows x 64 contiguous bytes.
+// This lane's share of one block of a wave: keys key0 + 16r (r < kKeysPerLane), each as kDP
+// 16-byte pieces: piece p = dims 32p + 8c .. 32p + 8c + 7 (bytes 64p + 16c).  A wave
+// instruction reads 16 rows x 64 contiguous bytes.
+template <int kDP>
 struct KV {
-  u32x4 k[kKeysPerLane][2], v[kKeysPerLane][2];
+  u32x4 k[kKeysPerLane][kDP], v[kKeysPerLane][kDP];
 };
 
 // kb: the block's first key (wave-uniform); k_lane/v_lane: this lane's byte offset within a
-// block, (l/4) * row + 16c; key r of the lane is 16r rows further.  A block that is not live loads from kOutOfRange (+ the
-// lane part, still past num_records as an unsigned 32-bit offset).
-__device__ __forceinline__ void load_block(KV& x, __amdgpu_buffer_rsrc_t kd,
+// block, (l/4) * row + 16c; key r of the lane is 16r rows further.  A block that is not live
+// loads from kOutOfRange (+ the lane part, still past num_records as an unsigned 32-bit
+// offset); so does a piece past the head dim (bit p of pmask clear).
+template <class Sh>
+__device__ __forceinline__ void load_block(KV<Sh::kDP>& x, __amdgpu_buffer_rsrc_t kd,
                                            __amdgpu_buffer_rsrc_t vd, int krow, int vrow, int kb,
-                                           bool live, int k_lane, int v_lane) {
-  const int ks = __builtin_amdgcn_readfirstlane(live ? kb * krow : kOutOfRange);
-  const int vs = __builtin_amdgcn_readfirstlane(live ? kb * vrow : kOutOfRange);
+                                           bool live, int k_lane, int v_lane, uint32_t pmask) {
+  const uint32_t ks = (uint32_t)__builtin_amdgcn_readfirstlane(live ? kb * krow : (int)kOutOfRange);
+  const uint32_t vs = (uint32_t)__builtin_amdgcn_readfirstlane(live ? kb * vrow : (int)kOutOfRange);
 #pragma unroll
   for (int r = 0; r < kKeysPerLane; ++r)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      x.k[r][p] = load16(kd, ks + k_lane + 16 * r * krow + 64 * p);
-      x.v[r][p] = load16(vd, vs + v_lane + 16 * r * vrow + 64 * p);
+    for (int p = 0; p < Sh::kDP; ++p) {
+      uint32_t ko = ks + (uint32_t)(k_lane + 16 * r * krow + 64 * p);
+      uint32_t vo = vs + (uint32_t)(v_lane + 16 * r * vrow + 64 * p);
+      if (Sh::kMaskD && !((pmask >> p) & 1u)) {
+        ko = kOutOfRange;
+        vo = kOutOfRange;
+      }
+      x.k[r][p] = load16(kd, ko);
+      x.v[r][p] = load16(vd, vo);
     }
 }
 
-// bf16 pair helpers: v_dot2_f32_bf16 (a.lo*b.lo + a.hi*b.hi + c, fp32 accumulate; products
-// of bf16 values are exact in fp32) and v_perm_b32 byte selection.
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
-                                         __builtin_bit_cast(bf16x2, b), c, false);
-}
-// (x.lo16, y.lo16) and (x.hi16, y.hi16): one head dim of two keys side by side.
+// (x.lo16, y.lo16) and (x.hi16, y.hi16): one head dim of two keys side by side (v_perm_b32).
 __device__ __forceinline__ uint32_t pair_lo(uint32_t x, uint32_t y) {
   return __builtin_amdgcn_perm(y, x, 0x05040100u);
 }
@@ -148,26 +194,31 @@ __device__ __forceinline__ uint32_t pair_hi(uint32_t x, uint32_t y) {
   return __builtin_amdgcn_perm(y, x, 0x07060302u);
 }
 
-// Online-softmax update of this key column's stream (m, l, o[16]) with the lane's keys of
+// Online-softmax update of this key column's stream (m, l, o[8 kDP]) with the lane's keys of
 // the block.
-//   scores: q . k as bf16 dot2 (q kept in bf16, exact products), times scale*log2(e);
-//   o += p_r v_r + p_r+1 v_r+1 as bf16 dot2 of (p_r, p_r+1) with (v_r[d], v_r+1[d]) built by
-//   v_perm; p is rounded to bf16 for that product (as the forward kernel's P operand), l sums
-//   it in fp32.
+//   scores: q . k as dot2 of element pairs (q kept in the element type, exact products),
+//   times scale*log2(e); even pieces accumulate in one sum, odd pieces in another;
+//   o += p_r v_r + p_r+1 v_r+1 as dot2 of (p_r, p_r+1) with (v_r[d], v_r+1[d]) built by
+//   v_perm; p is rounded to the element type for that product (as the forward kernel's P
+//   operand), l sums it in fp32.
 //   The running max is exact, so the largest weight of the stream is exactly 1.
 //   o and l are rescaled only when some lane's max moved (wave-uniform test).
-__device__ __forceinline__ void block_update(const KV& x, const uint32_t (&qp)[8],
+template <class Sh>
+__device__ __forceinline__ void block_update(const KV<Sh::kDP>& x, const uint32_t (&qp)[4 * Sh::kDP],
                                              float scale_log2, int key0, int key_end, float& m,
-                                             float& l, float (&o)[16]) {
+                                             float& l, float (&o)[8 * Sh::kDP]) {
+  typedef typename Sh::T T;
   float s[kKeysPerLane];
 #pragma unroll
   for (int r = 0; r < kKeysPerLane; ++r) {
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc0 = dot2(qp[i], x.k[r][0][i], acc0);
-      acc1 = dot2(qp[4 + i], x.k[r][1][i], acc1);
-    }
+    for (int p = 0; p < Sh::kDP; p += 2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc0 = DElem<T>::dot2(qp[4 * p + i], x.k[r][p][i], acc0);
+        acc1 = DElem<T>::dot2(qp[4 * p + 4 + i], x.k[r][p + 1][i], acc1);
+      }
     const float acc = quad_sum(acc0 + acc1) * scale_log2;
     s[r] = (key0 + 16 * r < key_end) ? acc : -INFINITY;
   }
@@ -179,37 +230,45 @@ __device__ __forceinline__ void block_update(const KV& x, const uint32_t (&qp)[8
     const float alpha = exp2f(m - m_use);
     l *= alpha;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] *= alpha;
+    for (int i = 0; i < 8 * Sh::kDP; ++i) o[i] *= alpha;
   }
 #pragma unroll
   for (int r = 0; r < kKeysPerLane; r += 2) {
     const float p0 = exp2f(s[r] - m_use), p1 = exp2f(s[r + 1] - m_use);
     l += p0 + p1;
-    const bf16x2 pb = {(__bf16)p0, (__bf16)p1};
-    const uint32_t pp = __builtin_bit_cast(uint32_t, pb);
+    T pe[2] = {(T)p0, (T)p1};
+    const uint32_t pp = (uint32_t)__builtin_bit_cast(unsigned short, pe[0]) |
+                        ((uint32_t)__builtin_bit_cast(unsigned short, pe[1]) << 16);
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int p = 0; p < Sh::kDP; ++p)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        o[8 * p + 2 * i] = dot2(pp, pair_lo(x.v[r][p][i], x.v[r + 1][p][i]), o[8 * p + 2 * i]);
+        o[8 * p + 2 * i] =
+            DElem<T>::dot2(pp, pair_lo(x.v[r][p][i], x.v[r + 1][p][i]), o[8 * p + 2 * i]);
         o[8 * p + 2 * i + 1] =
-            dot2(pp, pair_hi(x.v[r][p][i], x.v[r + 1][p][i]), o[8 * p + 2 * i + 1]);
+            DElem<T>::dot2(pp, pair_hi(x.v[r][p][i], x.v[r + 1][p][i]), o[8 * p + 2 * i + 1]);
       }
   }
   m = m_new;
 }
 
 // The new token as one more key of the stream of key column 0 (lanes 0..3) of the calling
-// wave; every other column sees it masked.  kn/vn: this lane's pieces of k_new and v_new.
-__device__ __forceinline__ void new_key_update(const u32x4 (&kn)[2], const u32x4 (&vn)[2],
-                                               const uint32_t (&qp)[8], float scale_log2,
-                                               bool mine, float& m, float& l, float (&o)[16]) {
+// wave; every other column sees it masked.  kn/vn: this lane's pieces of k_new and v_new
+// (zero past the head dim).
+template <class Sh>
+__device__ __forceinline__ void new_key_update(const u32x4 (&kn)[Sh::kDP], const u32x4 (&vn)[Sh::kDP],
+                                               const uint32_t (&qp)[4 * Sh::kDP], float scale_log2,
+                                               bool mine, float& m, float& l,
+                                               float (&o)[8 * Sh::kDP]) {
+  typedef typename Sh::T T;
   float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    acc0 = dot2(qp[i], kn[0][i], acc0);
-    acc1 = dot2(qp[4 + i], kn[1][i], acc1);
-  }
+  for (int p = 0; p < Sh::kDP; p += 2)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc0 = DElem<T>::dot2(qp[4 * p + i], kn[p][i], acc0);
+      acc1 = DElem<T>::dot2(qp[4 * p + 4 + i], kn[p + 1][i], acc1);
+    }
   const float sc = mine ? quad_sum(acc0 + acc1) * scale_log2 : -INFINITY;
   const float m_new = fmaxf(m, sc);
   const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
@@ -217,37 +276,47 @@ __device__ __forceinline__ void new_key_update(const u32x4 (&kn)[2], const u32x4
   const float pn = exp2f(sc - m_use);
   l = fmaf(l, alpha, pn);
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
+  for (int p = 0; p < Sh::kDP; ++p)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      o[8 * p + 2 * i] = fmaf(pn, bf_lo(vn[p][i]), o[8 * p + 2 * i] * alpha);
-      o[8 * p + 2 * i + 1] = fmaf(pn, bf_hi(vn[p][i]), o[8 * p + 2 * i + 1] * alpha);
+      o[8 * p + 2 * i] = fmaf(pn, DElem<T>::lo(vn[p][i]), o[8 * p + 2 * i] * alpha);
+      o[8 * p + 2 * i + 1] = fmaf(pn, DElem<T>::hi(vn[p][i]), o[8 * p + 2 * i + 1] * alpha);
     }
   m = m_new;
 }
 
+// pstride: floats per partial (D + 1: o_s[D], lse_s).
+template <class Sh>
 __global__ __launch_bounds__(kThreads) void decode_kernel(
-    const __bf16* __restrict__ Q, Vecs qs, __bf16* Kc, Rows ks, __bf16* Vc, Rows vs,
-    const __bf16* __restrict__ Kn, Vecs kns, const __bf16* __restrict__ Vn, Vecs vns,
-    const int* __restrict__ seqlens, __bf16* __restrict__ O, Vecs os, float* __restrict__ LSE,
-    float* __restrict__ part, int H, int N_max, int S, int C, float scale_log2) {
+    const typename Sh::T* __restrict__ Q, Vecs qs, typename Sh::T* Kc, Rows ks,
+    typename Sh::T* Vc, Rows vs, const typename Sh::T* __restrict__ Kn, Vecs kns,
+    const typename Sh::T* __restrict__ Vn, Vecs vns, const int* __restrict__ seqlens,
+    typename Sh::T* __restrict__ O, Vecs os, float* __restrict__ LSE, float* __restrict__ part,
+    int H, int N_max, int D, int S, int C, float scale_log2) {
+  typedef typename Sh::T T;
+  constexpr int kDP = Sh::kDP;
+  constexpr int kDm = Sh::kDm;
   constexpr int kStreams = kWaves * kGroups;       // softmax streams of the workgroup
-  constexpr int kParts = kThreads / kD;            // first-level merge: streams in kParts parts
+  constexpr int kParts = kThreads / kDm;           // first-level merge: streams in kParts parts
   constexpr int kPerPart = kStreams / kParts;
-  __shared__ float sh_o[kStreams][kD + 1];         // +1: stream-major writes, dim-major reads
+  __shared__ float sh_o[kStreams][kDm + 1];        // +1: stream-major writes, dim-major reads
   __shared__ float sh_m[kStreams], sh_l[kStreams];
-  __shared__ float sh_po[kParts][kD], sh_pm[kParts], sh_pl[kParts];
+  __shared__ float sh_po[kParts][kDm], sh_pm[kParts], sh_pl[kParts];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 2;  // key column within the wave
-  const int c = lane & 3;   // dims 8c .. 8c+7 and 32+8c .. 32+8c+7
+  const int c = lane & 3;   // dims 32p + 8c .. 32p + 8c + 7 of each piece p
 
   const int bh = blockIdx.x / S;
   const int s = blockIdx.x - bh * S;
   const int b = bh / H, h = bh - b * H;
   const bool append = Kn != nullptr;
+  // Pieces of this lane inside the head dim: bit p set when dims 32p + 8c.. are below D.
+  uint32_t pmask = 0;
+#pragma unroll
+  for (int p = 0; p < kDP; ++p) pmask |= (uint32_t)(!Sh::kMaskD || 32 * p + 8 * c < D) << p;
 
   const int Lc = seqlens ? seqlens[b] : N_max;  // valid cached rows
   const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
@@ -255,51 +324,57 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   const int c0 = s * C;
   const int c1 = min(c0 + C, L);
 
-  __bf16* Kh = Kc + b * ks.b + h * ks.h;
-  __bf16* Vh = Vc + b * vs.b + h * vs.h;
+  T* Kh = Kc + b * ks.b + h * ks.h;
+  T* Vh = Vc + b * vs.b + h * vs.h;
   const int krow = (int)ks.n * 2, vrow = (int)vs.n * 2;
   const int Lr = valid ? Lc : 0;
   const __amdgpu_buffer_rsrc_t kd = rows_rsrc(Kh, Lr * krow);
   const __amdgpu_buffer_rsrc_t vd = rows_rsrc(Vh, Lr * vrow);
 
   // The new token: stored into the cache by the workgroup whose chunk holds row Lc.
-  u32x4 k_app[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, v_app[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+  u32x4 k_app[kDP], v_app[kDP];
+#pragma unroll
+  for (int p = 0; p < kDP; ++p) {
+    k_app[p] = u32x4{0, 0, 0, 0};
+    v_app[p] = u32x4{0, 0, 0, 0};
+  }
   const bool has_new = append && valid && Lc >= c0 && Lc < c0 + C;
   if (has_new) {
-    const __bf16* kn = Kn + b * kns.b + h * kns.h;
-    const __bf16* vn = Vn + b * vns.b + h * vns.h;
+    const T* kn = Kn + b * kns.b + h * kns.h;
+    const T* vn = Vn + b * vns.b + h * vns.h;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      k_app[p] = *reinterpret_cast<const u32x4*>(kn + 32 * p + 8 * c);
-      v_app[p] = *reinterpret_cast<const u32x4*>(vn + 32 * p + 8 * c);
-    }
+    for (int p = 0; p < kDP; ++p)
+      if ((pmask >> p) & 1u) {
+        k_app[p] = *reinterpret_cast<const u32x4*>(kn + 32 * p + 8 * c);
+        v_app[p] = *reinterpret_cast<const u32x4*>(vn + 32 * p + 8 * c);
+      }
     if (wave == 0 && g == 0) {
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        *reinterpret_cast<u32x4*>(Kh + (long long)Lc * ks.n + 32 * p + 8 * c) = k_app[p];
-        *reinterpret_cast<u32x4*>(Vh + (long long)Lc * vs.n + 32 * p + 8 * c) = v_app[p];
-      }
+      for (int p = 0; p < kDP; ++p)
+        if ((pmask >> p) & 1u) {
+          *reinterpret_cast<u32x4*>(Kh + (long long)Lc * ks.n + 32 * p + 8 * c) = k_app[p];
+          *reinterpret_cast<u32x4*>(Vh + (long long)Lc * vs.n + 32 * p + 8 * c) = v_app[p];
+        }
     }
   }
 
-  uint32_t qp[8];  // this lane's q pieces as bf16 pairs (dims 8c.. and 32+8c..)
+  uint32_t qp[4 * kDP];  // this lane's q pieces as element pairs (zero past the head dim)
   {
-    const __bf16* qh = Q + b * qs.b + h * qs.h;
+    const T* qh = Q + b * qs.b + h * qs.h;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const u32x4 qv = *reinterpret_cast<const u32x4*>(qh + 32 * p + 8 * c);
+    for (int p = 0; p < kDP; ++p) {
+      u32x4 qv = {0, 0, 0, 0};
+      if ((pmask >> p) & 1u) qv = *reinterpret_cast<const u32x4*>(qh + 32 * p + 8 * c);
 #pragma unroll
       for (int i = 0; i < 4; ++i) qp[4 * p + i] = qv[i];
     }
   }
 
-  float m = -INFINITY, l = 0.f, o[16];
+  float m = -INFINITY, l = 0.f, o[8 * kDP];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = 0.f;
+  for (int i = 0; i < 8 * kDP; ++i) o[i] = 0.f;
 
-  // Blocks of this wave: kb = c0 + 32*wave + 128*t.  Two register sets used in turn, so the
-  // next block's loads are in flight while the current one is computed, with no copies
-  // between the sets (a copy would wait for the loads).
+  // Blocks of this wave: kb = c0 + 32*wave + 128*t.
   // Cached rows of this chunk: [c0, ce).  The appended row (Lc, if it falls in this chunk) is
   // not read from the cache; wave 0 folds it in after the loop.
   const int ce = min(c1, Lc);
@@ -309,35 +384,37 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     const int k_lane = g * krow + 16 * c;
     const int v_lane = g * vrow + 16 * c;
     // Two register sets used in turn: the next block's loads are in flight while one block
-    // is computed.  Pairs of blocks per iteration, one back edge and no exit inside the body,
-    // so at the top of an iteration only A's loads are outstanding.  (A third set was measured
-    // slower: the compiler then waits for two sets before the first block of an iteration.)
-    KV A, B;
-    load_block(A, kd, vd, krow, vrow, kb, true, k_lane, v_lane);
+    // is computed, with no copies between the sets (a copy would wait for the loads).  Pairs
+    // of blocks per iteration, one back edge and no exit inside the body, so at the top of an
+    // iteration only A's loads are outstanding.  (A third set was measured slower: the
+    // compiler then waits for two sets before the first block of an iteration.)
+    KV<kDP> A, B;
+    load_block<Sh>(A, kd, vd, krow, vrow, kb, true, k_lane, v_lane, pmask);
     // The scheduling barriers keep each block's arithmetic after the loads issued before it:
     // left alone, the scheduler hoists the (independent) dot products of the next block, which
     // then wait for the loads just issued.
     for (int t = 0; t + 2 <= nblk; t += 2) {
-      load_block(B, kd, vd, krow, vrow, kb + kBlockKeys, true, k_lane, v_lane);
+      load_block<Sh>(B, kd, vd, krow, vrow, kb + kBlockKeys, true, k_lane, v_lane, pmask);
       __builtin_amdgcn_sched_barrier(0);
-      block_update(A, qp, scale_log2, kb + g, ce, m, l, o);
+      block_update<Sh>(A, qp, scale_log2, kb + g, ce, m, l, o);
       __builtin_amdgcn_sched_barrier(0);
       kb += kBlockKeys;
-      load_block(A, kd, vd, krow, vrow, kb + kBlockKeys, t + 2 < nblk, k_lane, v_lane);
+      load_block<Sh>(A, kd, vd, krow, vrow, kb + kBlockKeys, t + 2 < nblk, k_lane, v_lane, pmask);
       __builtin_amdgcn_sched_barrier(0);
-      block_update(B, qp, scale_log2, kb + g, ce, m, l, o);
+      block_update<Sh>(B, qp, scale_log2, kb + g, ce, m, l, o);
       __builtin_amdgcn_sched_barrier(0);
       kb += kBlockKeys;
     }
-    if (nblk & 1) block_update(A, qp, scale_log2, kb + g, ce, m, l, o);
+    if (nblk & 1) block_update<Sh>(A, qp, scale_log2, kb + g, ce, m, l, o);
   }
-  if (has_new && wave == 0) new_key_update(k_app, v_app, qp, scale_log2, g == 0, m, l, o);
+  if (has_new && wave == 0) new_key_update<Sh>(k_app, v_app, qp, scale_log2, g == 0, m, l, o);
 
   // Merge the workgroup's 128 streams (16 key columns x 8 waves): every stream to LDS; thread
-  // t folds streams [16*(t/64), +16) for head dim t%64; 64 threads fold the 8 results.
+  // t folds streams [kPerPart*(t/kDm), +kPerPart) for head dim t%kDm; kDm threads fold the
+  // kParts results.
   const int stream = wave * kGroups + g;
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
+  for (int p = 0; p < kDP; ++p)
 #pragma unroll
     for (int i = 0; i < 8; ++i) sh_o[stream][32 * p + 8 * c + i] = o[8 * p + i];
   if (c == 0) {
@@ -346,27 +423,27 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   }
   __syncthreads();
   {
-    const int d = tid & (kD - 1), part = tid / kD;
+    const int d = tid & (kDm - 1), pt = tid / kDm;
     float M = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kPerPart; ++i) M = fmaxf(M, sh_m[part * kPerPart + i]);
+    for (int i = 0; i < kPerPart; ++i) M = fmaxf(M, sh_m[pt * kPerPart + i]);
     const float M_use = (M == -INFINITY) ? 0.f : M;
     float lt = 0.f, ot = 0.f;
 #pragma unroll
     for (int i = 0; i < kPerPart; ++i) {
-      const int st = part * kPerPart + i;
+      const int st = pt * kPerPart + i;
       const float w = exp2f(sh_m[st] - M_use);
       lt = fmaf(w, sh_l[st], lt);
       ot = fmaf(w, sh_o[st][d], ot);
     }
-    sh_po[part][d] = ot;
+    sh_po[pt][d] = ot;
     if (d == 0) {
-      sh_pm[part] = M;
-      sh_pl[part] = lt;
+      sh_pm[pt] = M;
+      sh_pl[pt] = lt;
     }
   }
   __syncthreads();
-  if (tid >= kD) return;
+  if (tid >= kDm || (Sh::kMaskD && tid >= D)) return;
   const int d = tid;
   float M = -INFINITY;
 #pragma unroll
@@ -382,73 +459,119 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   const float on = lt > 0.f ? ot / lt : 0.f;
   const float lse2 = lt > 0.f ? M + log2f(lt) : -INFINITY;
   if (S == 1) {
-    store_o(O + b * os.b + h * os.h + d, on, valid);
+    store_o<T>(O + b * os.b + h * os.h + d, on, valid);
     if (LSE != nullptr && d == 0) store_lse(LSE + bh, lse2 * kLn2, valid);
   } else {
-    float* pp = part + ((long long)bh * S + s) * kPartFloats;
+    float* pp = part + ((long long)bh * S + s) * (D + 1);
     pp[d] = on;
-    if (d == 0) pp[kD] = lse2;
+    if (d == 0) pp[D] = lse2;
   }
 }
 
-// Combines the S partials of each head: one wave per head, lane = head dim.
+// Wave-wide max / sum (butterfly over the 64 lanes).
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// Combines the S partials of each head: one wave per head.  The lanes read the S partial
+// log-sum-exps in parallel (max and weight sum by wave reductions) and stage the weights
+// 2^(lse_s - M) in LDS; then each lane folds the S partial values of its head dims, four
+// independent loads at a time.  (A loop over the partials, one dependent load per split,
+// cost ~1 us per 4 splits.)
+constexpr int kMaxSplits = 1024;
+template <class T>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
-    const float* __restrict__ part, const int* __restrict__ seqlens, __bf16* __restrict__ O,
-    Vecs os, float* __restrict__ LSE, int BH, int H, int N_max, int S, bool append) {
-  const int bh = blockIdx.x * (kMergeThreads / 64) + (threadIdx.x >> 6);
+    const float* __restrict__ part, const int* __restrict__ seqlens, T* __restrict__ O, Vecs os,
+    float* __restrict__ LSE, int BH, int H, int N_max, int D, int S, bool append) {
+  __shared__ float sh_w[kMergeThreads / 64][kMaxSplits];
+  const int wave = threadIdx.x >> 6;
+  const int bh = blockIdx.x * (kMergeThreads / 64) + wave;
   if (bh >= BH) return;
-  const int d = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63;
   const int b = bh / H, h = bh - b * H;
   const int Lc = seqlens ? seqlens[b] : N_max;
-  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
-  const float* p = part + (long long)bh * S * kPartFloats;
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, p[s * kPartFloats + kD]);
+  const int pstride = D + 1;
+  const float* p = part + (long long)bh * S * pstride;
+  float mx = -INFINITY;
+  for (int s = lane; s < S; s += 64) mx = fmaxf(mx, p[s * pstride + D]);
+  const float M = wave_max(mx);
   const float M_use = (M == -INFINITY) ? 0.f : M;
-  float wt = 0.f, ot = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const float w = exp2f(p[s * kPartFloats + kD] - M_use);
-    wt += w;
-    ot = fmaf(w, p[s * kPartFloats + d], ot);
+  float ws = 0.f;
+  for (int s = lane; s < S; s += 64) {
+    const float w = exp2f(p[s * pstride + D] - M_use);
+    sh_w[wave][s] = w;
+    ws += w;
   }
-  const float on = wt > 0.f ? ot / wt : 0.f;
-  store_o(O + b * os.b + h * os.h + d, on, valid);
-  if (LSE != nullptr && d == 0)
+  const float wt = wave_sum(ws);
+  // The weights are read by other lanes of the same wave: the writes complete first, and the
+  // asm's memory clobber keeps the compiler from moving the reads above them.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
+  for (int d = lane; d < D; d += 64) {
+    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+    int s = 0;
+    for (; s + 4 <= S; s += 4) {
+      const float x0 = p[s * pstride + d], x1 = p[(s + 1) * pstride + d];
+      const float x2 = p[(s + 2) * pstride + d], x3 = p[(s + 3) * pstride + d];
+      o0 = fmaf(sh_w[wave][s], x0, o0);
+      o1 = fmaf(sh_w[wave][s + 1], x1, o1);
+      o2 = fmaf(sh_w[wave][s + 2], x2, o2);
+      o3 = fmaf(sh_w[wave][s + 3], x3, o3);
+    }
+    for (; s < S; ++s) o0 = fmaf(sh_w[wave][s], p[s * pstride + d], o0);
+    const float ot = (o0 + o1) + (o2 + o3);
+    store_o<T>(O + b * os.b + h * os.h + d, wt > 0.f ? ot / wt : 0.f, valid);
+  }
+  if (LSE != nullptr && lane == 0)
     store_lse(LSE + bh, wt > 0.f ? (M + log2f(wt)) * kLn2 : -INFINITY, valid);
 }
 
 // ---------------------------------------------------------------------------------------
 // Host side.
 
-// Splits for a cache of N_max rows.  One 8-wave workgroup per head keeps 128 KiB of K/V
-// loads in flight, enough to stream at HBM rate from one CU, so heads are not split while
-// B*H covers at least half the CUs (no partials, no merge kernel).  Below that, a head is
-// split into chunks of about kSplitKeys rows, at most about one workgroup per CU: a
-// workgroup has a fixed cost of several microseconds (the cache_seqlens load before the first
-// address, the first loads' latency, the stream merge), so a split of fewer rows loses more
-// than its extra parallelism gains (measured: 1 x 16 heads x 8192 rows takes 15.4 us with 4
-// or 8 splits per head, 19.9 us with 16, 30.1 us with 32).  Chunks are a multiple of
-// kBlockKeys, no split is empty.
-constexpr int kSplitKeys = 2048;
-static void choose_split(int BH, int N_max, int cu_count, int max_splits, int* S_out, int* C_out) {
+// Splits for a cache of N_max rows of head dim D.  One 8-wave workgroup per head keeps 128 KiB
+// of K/V loads in flight, enough to stream at HBM rate from one CU, so heads are not split
+// while B*H covers at least half the CUs (no partials, no merge kernel; measured: two splits
+// per head at B*H = 200 cost 30% more).  Below that, a head is split so that the workgroups
+// fill one round of the workgroup slots (two per CU for D <= 64, whose 120 VGPRs let two
+// 8-wave workgroups share a CU; one for D > 64), rounding down so that no slot runs two, and
+// no split holds less than kSplitBytes of K and V (one key block at least).  Measured with the
+// merge kernel below (graph-replayed steps, caches rotating through HBM): 1 x 16 heads x 8192
+// rows 18.6 us with 2048-row splits -> 13.7 us; D = 128, 1 x 16 x 8192: 32.9 -> 21.3 us;
+// 1 x 8 x 2048: 14.1 -> 8.9 us.  Chunks are a multiple of kBlockKeys, no split is empty.
+constexpr int kSplitBytes = 64 * 1024;
+static void choose_split(int BH, int N_max, int D, int cu_count, int max_splits, int* S_out,
+                         int* C_out) {
   const int blocks = std::max(1, (N_max + kBlockKeys - 1) / kBlockKeys);
-  int S = 2 * BH >= cu_count ? 1 : (cu_count + BH - 1) / BH;
-  S = std::min(S, (N_max + kSplitKeys - 1) / kSplitKeys);
+  int S = 1;
+  if (2 * BH < cu_count) {
+    const int slots = cu_count * (D <= 64 ? 2 : 1);
+    S = std::max(1, slots / BH);
+    const int split_keys = std::max(kBlockKeys, kSplitBytes / (4 * D));
+    S = std::min(S, (N_max + split_keys - 1) / split_keys);
+  }
   S = std::min(S, blocks);
-  S = std::max(1, std::min(S, max_splits));
+  S = std::max(1, std::min(std::min(S, max_splits), kMaxSplits));
   const int C = (blocks + S - 1) / S * kBlockKeys;
   S = std::max(1, (N_max + C - 1) / C);
   *S_out = S;
   *C_out = C;
 }
 
-static bool rows_ok(const int64_t* st, int B, int H, int N_max, Rows* out) {
+static bool rows_ok(const int64_t* st, int B, int H, int N_max, int D, Rows* out) {
   Rows r;
   r.b = B == 1 ? 0 : st[0];
   r.h = H == 1 ? 0 : st[1];
-  r.n = N_max <= 1 ? kD : st[2];
+  r.n = N_max <= 1 ? D : st[2];
   if (st[3] != 1) return false;
-  if (r.b < 0 || r.h < 0 || r.n < kD || ((r.b | r.h | r.n) & 7)) return false;
+  if (r.b < 0 || r.h < 0 || r.n < D || ((r.b | r.h | r.n) & 7)) return false;
   *out = r;
   return true;
 }
@@ -463,9 +586,9 @@ static bool vecs_ok(const int64_t* st, int B, int H, Vecs* out) {
   return true;
 }
 
-// O rows (64 elements each) must not share elements: sorted by stride, each stride of a
+// O rows (D elements each) must not share elements: sorted by stride, each stride of a
 // dimension of size > 1 is at least the span reached through the smaller one.
-static bool vecs_overlap(const Vecs& v, int B, int H) {
+static bool vecs_overlap(const Vecs& v, int B, int H, int D) {
   long long st[2] = {v.b, v.h}, sz[2] = {B, H};
   if (st[1] < st[0]) {
     const long long t = st[0], z = sz[0];
@@ -474,7 +597,7 @@ static bool vecs_overlap(const Vecs& v, int B, int H) {
     st[1] = t;
     sz[1] = z;
   }
-  long long reach = kD - 1;
+  long long reach = D - 1;
   for (int i = 0; i < 2; ++i) {
     if (sz[i] == 1) continue;
     if (st[i] <= reach) return true;
@@ -483,28 +606,20 @@ static bool vecs_overlap(const Vecs& v, int B, int H) {
   return false;
 }
 
-}  // namespace tfgfa_decode
+// Bytes of one partial set (every head, one split) for head dim D: o_s[D] and lse_s.
+static size_t split_bytes(long long bh, int D) { return (size_t)bh * (size_t)(D + 1) * sizeof(float); }
 
-extern "C" size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max) {
-  using namespace tfgfa_decode;
-  if (B <= 0 || H <= 0 || N_max <= 0) return 0;
-  // One partial per 128 cache rows: an upper bound on the splits of any block size >= 128,
-  // so the size does not change with the kernel's tiling.
-  const size_t blocks = ((size_t)N_max + kWorkspaceRows - 1) / kWorkspaceRows;
-  return (size_t)B * (size_t)H * blocks * kPartFloats * sizeof(float);
-}
-
-extern "C" int tfgfa_decode_bf16(const void* q, const int64_t* q_strides, void* k_cache,
-                                 const int64_t* k_strides, void* v_cache,
-                                 const int64_t* v_strides, const void* k_new,
-                                 const int64_t* k_new_strides, const void* v_new,
-                                 const int64_t* v_new_strides, const int* cache_seqlens, void* o,
-                                 const int64_t* o_strides, float* lse, int B, int H, int N_max,
-                                 int D, float softmax_scale, void* workspace,
-                                 size_t workspace_bytes, void* hip_stream) {
-  using namespace tfgfa_decode;
+// The decode step for one element type: argument checks, split choice, launches.
+template <class T>
+static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
+                       const int64_t* k_strides, void* v_cache, const int64_t* v_strides,
+                       const void* k_new, const int64_t* k_new_strides, const void* v_new,
+                       const int64_t* v_new_strides, const int* cache_seqlens, void* o,
+                       const int64_t* o_strides, float* lse, int B, int H, int N_max, int D,
+                       float softmax_scale, void* workspace, size_t workspace_bytes,
+                       void* hip_stream) {
   if (B < 0 || H < 0 || N_max < 0) return TFGFA_ERR_BAD_SHAPE;
-  if (D != kD) return TFGFA_ERR_HEAD_DIM;
+  if (D < 8 || D > kMaxD || (D & 7)) return TFGFA_ERR_HEAD_DIM;
   if (!(softmax_scale > 0.f) || !isfinite(softmax_scale)) return TFGFA_ERR_SCALE;
   if ((k_new == nullptr) != (v_new == nullptr)) return TFGFA_ERR_NULL_POINTER;
   const bool append = k_new != nullptr;
@@ -518,11 +633,11 @@ extern "C" int tfgfa_decode_bf16(const void* q, const int64_t* q_strides, void* 
   if (!q_strides || !k_strides || !v_strides || !o_strides) return TFGFA_ERR_NULL_POINTER;
   if (append && (!k_new_strides || !v_new_strides)) return TFGFA_ERR_NULL_POINTER;
   if (!vecs_ok(q_strides, B, H, &qs) || !vecs_ok(o_strides, B, H, &os)) return TFGFA_ERR_STRIDE;
-  if (!rows_ok(k_strides, B, H, N_max, &ks) || !rows_ok(v_strides, B, H, N_max, &vs))
+  if (!rows_ok(k_strides, B, H, N_max, D, &ks) || !rows_ok(v_strides, B, H, N_max, D, &vs))
     return TFGFA_ERR_STRIDE;
   if (append && (!vecs_ok(k_new_strides, B, H, &kns) || !vecs_ok(v_new_strides, B, H, &vns)))
     return TFGFA_ERR_STRIDE;
-  if (vecs_overlap(os, B, H)) return TFGFA_ERR_STRIDE;
+  if (vecs_overlap(os, B, H, D)) return TFGFA_ERR_STRIDE;
   // Cache rows are addressed with 32-bit buffer offsets (row index * row stride, plus a block).
   if (((long long)N_max + kBlockKeys) * ks.n * 2 > INT32_MAX ||
       ((long long)N_max + kBlockKeys) * vs.n * 2 > INT32_MAX)
@@ -537,31 +652,99 @@ extern "C" int tfgfa_decode_bf16(const void* q, const int64_t* q_strides, void* 
   int cu = 0;
   const int st = tfgfa_device_info(&cu, nullptr, nullptr, 0);
   if (st != TFGFA_OK) return st;
-  const size_t per_split = (size_t)bh * kPartFloats * sizeof(float);
+  const size_t per_split = split_bytes(bh, D);
   const int ws_splits =
       workspace ? (int)std::min((size_t)INT32_MAX, workspace_bytes / per_split) : 0;
   int S, C;
-  choose_split((int)bh, N_max, cu, std::max(1, ws_splits), &S, &C);
+  choose_split((int)bh, N_max, D, cu, std::max(1, ws_splits), &S, &C);
   if (bh * S > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
 
   const hipStream_t stream = (hipStream_t)hip_stream;
   const float scale_log2 = softmax_scale * kLog2e;
-  hipLaunchKernelGGL(decode_kernel, dim3((unsigned)(bh * S)), dim3(kThreads), 0, stream,
-                     static_cast<const __bf16*>(q), qs, static_cast<__bf16*>(k_cache), ks,
-                     static_cast<__bf16*>(v_cache), vs, static_cast<const __bf16*>(k_new), kns,
-                     static_cast<const __bf16*>(v_new), vns, cache_seqlens,
-                     static_cast<__bf16*>(o), os, lse, static_cast<float*>(workspace), H, N_max,
-                     S, C, scale_log2);
+  const T* qt = static_cast<const T*>(q);
+  T* kc = static_cast<T*>(k_cache);
+  T* vc = static_cast<T*>(v_cache);
+  const T* knt = static_cast<const T*>(k_new);
+  const T* vnt = static_cast<const T*>(v_new);
+  T* ot = static_cast<T*>(o);
+  float* ws = static_cast<float*>(workspace);
+  const dim3 grid((unsigned)(bh * S)), block(kThreads);
+#define TFGFA_DECODE_LAUNCH(kDP, kMask)                                                        \
+  hipLaunchKernelGGL((decode_kernel<DShape<T, kDP, kMask>>), grid, block, 0, stream, qt, qs, kc, \
+                     ks, vc, vs, knt, kns, vnt, vns, cache_seqlens, ot, os, lse, ws, H, N_max, D, \
+                     S, C, scale_log2)
+  if (D == 64)
+    TFGFA_DECODE_LAUNCH(2, false);
+  else if (D < 64)
+    TFGFA_DECODE_LAUNCH(2, true);
+  else if (D == 128)
+    TFGFA_DECODE_LAUNCH(4, false);
+  else
+    TFGFA_DECODE_LAUNCH(4, true);
+#undef TFGFA_DECODE_LAUNCH
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return -(int)e;
   if (S > 1) {
     const int heads_per_wg = kMergeThreads / 64;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((bh + heads_per_wg - 1) / heads_per_wg)),
+    hipLaunchKernelGGL(decode_merge_kernel<T>,
+                       dim3((unsigned)((bh + heads_per_wg - 1) / heads_per_wg)),
                        dim3(kMergeThreads), 0, stream, static_cast<const float*>(workspace),
-                       cache_seqlens, static_cast<__bf16*>(o), os, lse, (int)bh, H, N_max, S,
-                       append);
+                       cache_seqlens, ot, os, lse, (int)bh, H, N_max, D, S, append);
     e = hipGetLastError();
     if (e != hipSuccess) return -(int)e;
   }
   return TFGFA_OK;
+}
+
+}  // namespace tfgfa_dec
+
+extern "C" size_t tfgfa_decode_workspace_size(int B, int H, int N_max, int D) {
+  using namespace tfgfa_dec;
+  if (B <= 0 || H <= 0 || N_max <= 0 || D < 8 || D > kMaxD || (D & 7)) return 0;
+  // One partial per 128 cache rows: an upper bound on the splits of any block size >= 128,
+  // so the size does not change with the kernel's tiling.
+  const size_t blocks = ((size_t)N_max + kWorkspaceRows - 1) / kWorkspaceRows;
+  return split_bytes((long long)B * H, D) * blocks;
+}
+
+extern "C" size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max) {
+  return tfgfa_decode_workspace_size(B, H, N_max, tfgfa_dec::kD);
+}
+
+extern "C" int tfgfa_decode_bf16(const void* q, const int64_t* q_strides, void* k_cache,
+                                 const int64_t* k_strides, void* v_cache,
+                                 const int64_t* v_strides, const void* k_new,
+                                 const int64_t* k_new_strides, const void* v_new,
+                                 const int64_t* v_new_strides, const int* cache_seqlens, void* o,
+                                 const int64_t* o_strides, float* lse, int B, int H, int N_max,
+                                 int D, float softmax_scale, void* workspace,
+                                 size_t workspace_bytes, void* hip_stream) {
+  if (B < 0 || H < 0 || N_max < 0) return TFGFA_ERR_BAD_SHAPE;
+  if (D != tfgfa_dec::kD) return TFGFA_ERR_HEAD_DIM;
+  return tfgfa_dec::decode_step<__bf16>(q, q_strides, k_cache, k_strides, v_cache, v_strides,
+                                           k_new, k_new_strides, v_new, v_new_strides,
+                                           cache_seqlens, o, o_strides, lse, B, H, N_max, D,
+                                           softmax_scale, workspace, workspace_bytes, hip_stream);
+}
+
+extern "C" int tfgfa_decode(const void* q, const int64_t* q_strides, void* k_cache,
+                            const int64_t* k_strides, void* v_cache, const int64_t* v_strides,
+                            const void* k_new, const int64_t* k_new_strides, const void* v_new,
+                            const int64_t* v_new_strides, const int* cache_seqlens, void* o,
+                            const int64_t* o_strides, float* lse, int B, int H, int N_max, int D,
+                            int dtype, float softmax_scale, void* workspace,
+                            size_t workspace_bytes, void* hip_stream) {
+  if (dtype == TFGFA_DTYPE_BF16)
+    return tfgfa_dec::decode_step<__bf16>(q, q_strides, k_cache, k_strides, v_cache,
+                                             v_strides, k_new, k_new_strides, v_new,
+                                             v_new_strides, cache_seqlens, o, o_strides, lse, B, H,
+                                             N_max, D, softmax_scale, workspace, workspace_bytes,
+                                             hip_stream);
+  if (dtype == TFGFA_DTYPE_F16)
+    return tfgfa_dec::decode_step<_Float16>(q, q_strides, k_cache, k_strides, v_cache,
+                                               v_strides, k_new, k_new_strides, v_new,
+                                               v_new_strides, cache_seqlens, o, o_strides, lse, B,
+                                               H, N_max, D, softmax_scale, workspace,
+                                               workspace_bytes, hip_stream);
+  return TFGFA_ERR_DTYPE;
 }

@@ -100,6 +100,29 @@ void decode(std::uintptr_t q, const Strides3& qs, std::uintptr_t kc, const Strid
   }
 }
 
+void decode_general(std::uintptr_t q, const Strides3& qs, std::uintptr_t kc, const Strides4& ks,
+                    std::uintptr_t vc, const Strides4& vs, std::uintptr_t kn, const Strides3& kns,
+                    std::uintptr_t vn, const Strides3& vns, std::uintptr_t seqlens,
+                    std::uintptr_t o, const Strides3& os, std::uintptr_t lse, int B, int H,
+                    int N_max, int D, int dtype, float softmax_scale, std::uintptr_t workspace,
+                    std::size_t workspace_bytes, std::uintptr_t stream) {
+  int st;
+  {
+    py::gil_scoped_release nogil;
+    st = tfgfa_decode(
+        reinterpret_cast<const void*>(q), qs.data(), reinterpret_cast<void*>(kc), ks.data(),
+        reinterpret_cast<void*>(vc), vs.data(), reinterpret_cast<const void*>(kn), kns.data(),
+        reinterpret_cast<const void*>(vn), vns.data(), reinterpret_cast<const int*>(seqlens),
+        reinterpret_cast<void*>(o), os.data(), reinterpret_cast<float*>(lse), B, H, N_max, D,
+        dtype, softmax_scale, reinterpret_cast<void*>(workspace), workspace_bytes,
+        reinterpret_cast<void*>(stream));
+  }
+  if (st != TFGFA_OK) {
+    throw std::runtime_error(std::string("tfgfa_decode failed (status ") + std::to_string(st) +
+                             "): " + tfgfa_strerror(st));
+  }
+}
+
 py::dict device_info() {
   int cu = 0, mhz = 0;
   char arch[128] = {0};
@@ -144,8 +167,19 @@ PYBIND11_MODULE(_C, m) {
         py::arg("o_strides"), py::arg("lse"), py::arg("B"), py::arg("H"), py::arg("N_max"),
         py::arg("D"), py::arg("softmax_scale"), py::arg("workspace"),
         py::arg("workspace_bytes"), py::arg("stream"));
+  m.def("decode_general", &decode_general,
+        "One decode step, bf16/fp16, head dim a multiple of 8 up to 128 (element strides)",
+        py::arg("q"), py::arg("q_strides"), py::arg("k_cache"), py::arg("k_strides"),
+        py::arg("v_cache"), py::arg("v_strides"), py::arg("k_new"), py::arg("k_new_strides"),
+        py::arg("v_new"), py::arg("v_new_strides"), py::arg("cache_seqlens"), py::arg("o"),
+        py::arg("o_strides"), py::arg("lse"), py::arg("B"), py::arg("H"), py::arg("N_max"),
+        py::arg("D"), py::arg("dtype"), py::arg("softmax_scale"), py::arg("workspace"),
+        py::arg("workspace_bytes"), py::arg("stream"));
   m.def("decode_workspace_bytes", [](int B, int H, int N_max) {
     return tfgfa_decode_workspace_bytes(B, H, N_max);
+  });
+  m.def("decode_workspace_size", [](int B, int H, int N_max, int D) {
+    return tfgfa_decode_workspace_size(B, H, N_max, D);
   });
   m.def("device_info", &device_info, "CU count, shader clock (MHz) and arch of the current device");
   m.def("strerror", [](int st) { return std::string(tfgfa_strerror(st)); });

@@ -208,13 +208,13 @@ def flash_attn_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, softma
     return attention(q, k, v, out=o, softmax_scale=softmax_scale, causal=True)
 
 
-def _check_vec(x, name: str, B: int, H: int, dev) -> None:
+def _check_vec(x, name: str, B: int, H: int, D: int, dtype, dev) -> None:
     if not x.is_cuda:
         raise RuntimeError(f"{name} must be a CUDA tensor")
-    if x.dtype != torch.bfloat16:
-        raise RuntimeError("Unsupported tensor dtype. Use bfloat16.")
-    if tuple(x.shape) != (B, H, HEAD_DIM):
-        raise RuntimeError(f"{name} must have shape {(B, H, HEAD_DIM)}, got {tuple(x.shape)}")
+    if x.dtype != dtype:
+        raise RuntimeError(f"{name} must have dtype {dtype}, got {x.dtype}")
+    if tuple(x.shape) != (B, H, D):
+        raise RuntimeError(f"{name} must have shape {(B, H, D)}, got {tuple(x.shape)}")
     if x.device != dev:
         raise RuntimeError(f"{name} must be on {dev}, got {x.device}")
     if x.stride(2) != 1:
@@ -228,41 +228,46 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
            workspace: torch.Tensor | None = None):
     """One decode step: attention of one new query per (batch, head) over a KV cache.
 
-    ``q``: (B, H, 64) bf16.  ``k_cache``, ``v_cache``: (B, H, N_max, 64) bf16 views (any
-    strides with a dense last dimension, e.g. (B, N_max, H, 64) buffers transposed).
+    ``q``: (B, H, D).  ``k_cache``, ``v_cache``: (B, H, N_max, D) views (any strides with a
+    dense last dimension, e.g. (B, N_max, H, D) buffers transposed).  bf16 or fp16, all
+    operands alike; D a multiple of 8 up to 128 (GPT-2: bf16, D = 64).
     ``cache_seqlens``: int32 (B,) on the device, the number of valid cached rows per batch
-    row (``None``: all N_max rows).  With ``k_new``/``v_new`` ((B, H, 64) bf16) the new token is
+    row (``None``: all N_max rows).  With ``k_new``/``v_new`` ((B, H, D)) the new token is
     written into cache row ``cache_seqlens[b]`` first and attended too; the caller advances
-    ``cache_seqlens`` afterwards.  Returns ``out`` ((B, H, 64), new if not given), or
+    ``cache_seqlens`` afterwards.  Returns ``out`` ((B, H, D), new if not given), or
     ``(out, lse)`` with ``return_lse=True`` (lse (B, H) float32, natural log).  The result
     equals the last row of the causal forward over the first L tokens - what the reference's
     generate() recomputes from scratch for every token (src/py/model_inference.py:199-228).
     A length that does not fit the cache yields NaN for that batch row (checked on the device).
     ``workspace``: optional uint8 device buffer for split-sequence partials (no initialisation
     needed; an empty one runs each head as one workgroup); when absent, a buffer of
-    ``_C.decode_workspace_bytes(B, H, N_max)`` bytes is kept per device and stream and reused.
+    ``_C.decode_workspace_size(B, H, N_max, D)`` bytes is kept per device and stream and reused.
     """
     for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
         if not t.is_cuda:
             raise RuntimeError(f"{n} must be a CUDA tensor")
-        if t.dtype != torch.bfloat16:
-            raise RuntimeError("Unsupported tensor dtype. Use bfloat16.")
-        if t.dim() != 4 or t.shape[3] != HEAD_DIM:
-            raise RuntimeError(f"{n} must be (B, H, N_max, {HEAD_DIM}), got {tuple(t.shape)}")
+        if t.dtype not in _DTYPES:
+            raise RuntimeError("Unsupported tensor dtype. Use bfloat16 or float16.")
+        if t.dim() != 4:
+            raise RuntimeError(f"{n} must be (B, H, N_max, D), got {tuple(t.shape)}")
         if t.stride(3) != 1:
             raise RuntimeError(f"{n} must be dense in its last dimension (stride 1), got strides {t.stride()}")
     B, H, N_max, D = k_cache.shape
+    if not (8 <= D <= MAX_HEAD_DIM and D % 8 == 0):
+        raise RuntimeError(f"head_dim must be a multiple of 8 in [8, {MAX_HEAD_DIM}], got {D}")
+    if v_cache.dtype != k_cache.dtype:
+        raise RuntimeError(f"v_cache must have dtype {k_cache.dtype}, got {v_cache.dtype}")
     if v_cache.shape != k_cache.shape:
         raise RuntimeError(f"v_cache must have shape {tuple(k_cache.shape)}, got {tuple(v_cache.shape)}")
-    dev = k_cache.device
+    dev, dtype = k_cache.device, k_cache.dtype
     if v_cache.device != dev:
         raise RuntimeError(f"v_cache must be on {dev}, got {v_cache.device}")
-    _check_vec(q, "q", B, H, dev)
+    _check_vec(q, "q", B, H, D, dtype, dev)
     if (k_new is None) != (v_new is None):
         raise RuntimeError("k_new and v_new must be given together")
     if k_new is not None:
-        _check_vec(k_new, "k_new", B, H, dev)
-        _check_vec(v_new, "v_new", B, H, dev)
+        _check_vec(k_new, "k_new", B, H, D, dtype, dev)
+        _check_vec(v_new, "v_new", B, H, D, dtype, dev)
         if cache_seqlens is None:
             raise RuntimeError("appending k_new/v_new needs cache_seqlens")
     if cache_seqlens is not None:
@@ -271,26 +276,26 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         if cache_seqlens.device != dev or not cache_seqlens.is_contiguous():
             raise RuntimeError(f"cache_seqlens must be a contiguous tensor on {dev}")
     if out is None:
-        out = torch.empty((B, H, D), dtype=torch.bfloat16, device=dev)
+        out = torch.empty((B, H, D), dtype=dtype, device=dev)
     else:
-        _check_vec(out, "out", B, H, dev)
+        _check_vec(out, "out", B, H, D, dtype, dev)
     scale = (1.0 / math.sqrt(D)) if softmax_scale is None else float(softmax_scale)
     lse = torch.empty((B, H), dtype=torch.float32, device=dev) if return_lse else None
     if workspace is None:
-        workspace = _decode_workspace(dev, _C.decode_workspace_bytes(B, H, N_max))
+        workspace = _decode_workspace(dev, _C.decode_workspace_size(B, H, N_max, D))
     elif not workspace.is_cuda or workspace.device != dev or not workspace.is_contiguous():
         raise RuntimeError(f"workspace must be a contiguous tensor on {dev}")
     zero3 = (0, 0, 0)
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
-        _C.decode(
+        _C.decode_general(
             q.data_ptr(), q.stride(), k_cache.data_ptr(), k_cache.stride(),
             v_cache.data_ptr(), v_cache.stride(),
             0 if k_new is None else k_new.data_ptr(), zero3 if k_new is None else k_new.stride(),
             0 if v_new is None else v_new.data_ptr(), zero3 if v_new is None else v_new.stride(),
             0 if cache_seqlens is None else cache_seqlens.data_ptr(),
             out.data_ptr(), out.stride(), 0 if lse is None else lse.data_ptr(),
-            B, H, N_max, D, scale,
+            B, H, N_max, D, _DTYPES[dtype], scale,
             workspace.data_ptr() if workspace.numel() else 0,
             workspace.numel() * workspace.element_size(), stream,
         )
