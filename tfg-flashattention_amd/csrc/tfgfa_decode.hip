@@ -285,6 +285,31 @@ __device__ __forceinline__ void new_key_update(const u32x4 (&kn)[Sh::kDP], const
   m = m_new;
 }
 
+// Largest value over the 64 lanes of x when x is the same in the 4 lanes of each quad: row
+// rotations by 4 and 8 (DPP) give every lane its 16-lane row's maximum, then the 4 rows are
+// read as scalars.
+__device__ __forceinline__ float wave_max_quads(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false)));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Wave-wide max / sum (butterfly over the 64 lanes).
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
 // pstride: floats per partial (D + 1: o_s[D], lse_s).
 template <class Sh>
 __global__ __launch_bounds__(kThreads) void decode_kernel(
@@ -300,7 +325,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   constexpr int kParts = kThreads / kDm;           // first-level merge: streams in kParts parts
   constexpr int kPerPart = kStreams / kParts;
   __shared__ float sh_o[kStreams][kDm + 1];        // +1: stream-major writes, dim-major reads
-  __shared__ float sh_m[kStreams], sh_l[kStreams];
+  __shared__ float sh_l[kStreams], sh_wm[kWaves];
   __shared__ float sh_po[kParts][kDm], sh_pm[kParts], sh_pl[kParts];
 
   const int tid = threadIdx.x;
@@ -409,36 +434,49 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   }
   if (has_new && wave == 0) new_key_update<Sh>(k_app, v_app, qp, scale_log2, g == 0, m, l, o);
 
-  // Merge the workgroup's 128 streams (16 key columns x 8 waves): every stream to LDS; thread
-  // t folds streams [kPerPart*(t/kDm), +kPerPart) for head dim t%kDm; kDm threads fold the
-  // kParts results.
+  // Merge the workgroup's 128 streams (16 key columns x 8 waves) in two LDS rounds:
+  //  1. each wave scales its streams once by 2^(m - M_w), M_w its largest stream maximum (row
+  //     rotations and lane reads, no LDS), and writes them to LDS; thread t sums the streams
+  //     of part t/kDm (kWavesPerPart whole waves) for head dim t%kDm, rescaling the waves'
+  //     sums to the part's maximum;
+  //  2. kDm threads fold the kParts partial sums with the log-sum-exp rule.
+  // (Folding the 128 streams pairwise with their own maxima cost 16 exponentials and 32 more
+  // LDS reads per thread, ~1 us per step at the bench shape.)
+  constexpr int kWavesPerPart = kPerPart / kGroups;
+  static_assert(kPerPart % kGroups == 0, "a part is whole waves");
   const int stream = wave * kGroups + g;
+  const float Mw = wave_max_quads(m);
+  const float sc = exp2f(m - ((Mw == -INFINITY) ? 0.f : Mw));  // 0 for a stream that saw no key
 #pragma unroll
   for (int p = 0; p < kDP; ++p)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sh_o[stream][32 * p + 8 * c + i] = o[8 * p + i];
-  if (c == 0) {
-    sh_m[stream] = m;
-    sh_l[stream] = l;
-  }
+    for (int i = 0; i < 8; ++i) sh_o[stream][32 * p + 8 * c + i] = o[8 * p + i] * sc;
+  if (c == 0) sh_l[stream] = l * sc;
+  if (lane == 0) sh_wm[wave] = Mw;
   __syncthreads();
   {
     const int d = tid & (kDm - 1), pt = tid / kDm;
-    float M = -INFINITY;
+    float Mp = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kPerPart; ++i) M = fmaxf(M, sh_m[pt * kPerPart + i]);
-    const float M_use = (M == -INFINITY) ? 0.f : M;
-    float lt = 0.f, ot = 0.f;
+    for (int ww = 0; ww < kWavesPerPart; ++ww) Mp = fmaxf(Mp, sh_wm[pt * kWavesPerPart + ww]);
+    const float Mp_use = (Mp == -INFINITY) ? 0.f : Mp;
+    float ot = 0.f, lt = 0.f;
 #pragma unroll
-    for (int i = 0; i < kPerPart; ++i) {
-      const int st = pt * kPerPart + i;
-      const float w = exp2f(sh_m[st] - M_use);
-      lt = fmaf(w, sh_l[st], lt);
-      ot = fmaf(w, sh_o[st][d], ot);
+    for (int ww = 0; ww < kWavesPerPart; ++ww) {
+      const int w0 = (pt * kWavesPerPart + ww) * kGroups;
+      float os_ = 0.f, ls = 0.f;
+#pragma unroll
+      for (int i = 0; i < kGroups; ++i) os_ += sh_o[w0 + i][d];
+      if (d == 0)
+#pragma unroll
+        for (int i = 0; i < kGroups; ++i) ls += sh_l[w0 + i];
+      const float f = kWavesPerPart == 1 ? 1.f : exp2f(sh_wm[pt * kWavesPerPart + ww] - Mp_use);
+      ot = fmaf(f, os_, ot);
+      lt = fmaf(f, ls, lt);
     }
     sh_po[pt][d] = ot;
     if (d == 0) {
-      sh_pm[pt] = M;
+      sh_pm[pt] = Mp;
       sh_pl[pt] = lt;
     }
   }
@@ -466,18 +504,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     pp[d] = on;
     if (d == 0) pp[D] = lse2;
   }
-}
-
-// Wave-wide max / sum (butterfly over the 64 lanes).
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  return x;
 }
 
 // Combines the S partials of each head: one wave per head.  The lanes read the S partial
