@@ -149,7 +149,10 @@ int tfgfa_fwd_bf16_strided(const void* q, const int64_t* q_strides,
  * L + 1 keys; the caller advances cache_seqlens afterwards.  L_b = 0 gives
  * O = 0 and LSE = -inf.  A length that does not fit (cache_seqlens[b] < 0 or
  * cache_seqlens[b] + append > N_max) is only visible on the device: that batch
- * row gets NaN in O and LSE, and nothing is appended or read for it.
+ * row gets NaN in O and LSE, and nothing is appended or attended for it.
+ * Cache rows at or past the length never reach the result, but the first rows
+ * of a chunk may be loaded (within the N_max rows of the cache) before the
+ * length is known.
  *
  * workspace: device memory for split-sequence partials (16-byte aligned), or
  * NULL.  The cache sequence is split over up to

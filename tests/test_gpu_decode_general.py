@@ -9,7 +9,8 @@ Q, K ~ N(0, 3^2) and V ~ N(0, 1).
 Covered per element type (bf16, fp16) and head dim (8, 40, 64, 96, 128): ragged lengths,
 the fused append (cache row written, nothing else touched), the split-sequence path against
 the one-workgroup path, strided caches (bitwise equal to contiguous ones), NaN rows for
-invalid lengths; and bf16 / D = 64 bitwise equal to the bf16 entry point.
+invalid lengths, NaN / inf in cache rows past the length (no effect); and bf16 / D = 64
+bitwise equal to the bf16 entry point.
 """
 import sys
 
@@ -159,6 +160,36 @@ def test_invalid_lengths_give_nan_rows_only(dt, D):
     assert torch.isfinite(o[1]).all() and torch.isfinite(lse[1]).all()
     assert torch.equal(kd[0], k_before[0]) and torch.equal(kd[2], k_before[2]), "invalid rows appended"
     assert torch.equal(kd[1, :, 30], kn[1]), "valid row not appended"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dt", list(DTYPES))
+@pytest.mark.parametrize("append", [False, True])
+def test_rows_past_the_length_never_reach_the_result(dt, D, append):
+    """Cache rows at or past cache_seqlens (the first block of a chunk is loaded before the
+    length is known) hold NaN / inf: the result is bitwise that of a cache holding zeros there."""
+    B, H, N_max, lens = 4, 3, 600, [5, 33, 300, 0]
+    _say(f"decode garbage past length {dt} D={D} append={append}")
+    q, kc, vc = _case(B, H, N_max, D, 140 + D, dt)
+    for b, L in enumerate(lens):
+        kc[b, :, L:] = 0.0
+        vc[b, :, L:] = 0.0
+    kz, vz = _dev(kc, dt), _dev(vc, dt)
+    kg, vg = kz.clone(), vz.clone()
+    for b, L in enumerate(lens):
+        kg[b, :, L:] = float("nan")
+        vg[b, :, L:] = float("inf")
+        vg[b, :, L + 1::2] = float("nan")
+    qd = _dev(q, dt)
+    kn = _dev(_rand((B, H, D), 150, dt, 3.0), dt) if append else None
+    vn = _dev(_rand((B, H, D), 151, dt), dt) if append else None
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    ref = custom_flash_attn.decode(qd, kz, vz, sl, kn, vn, return_lse=True)
+    got = custom_flash_attn.decode(qd, kg, vg, sl, kn, vn, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got[0][:3]).all()
+    assert torch.equal(got[0].view(torch.int16), ref[0].view(torch.int16))
+    assert torch.equal(got[1], ref[1])
 
 
 def test_bf16_d64_is_bitwise_the_bf16_entry():

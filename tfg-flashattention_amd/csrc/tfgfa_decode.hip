@@ -38,11 +38,13 @@
 // workgroup whose chunk holds it stores k_new/v_new into cache row L_b and folds the values
 // from the inputs into one softmax stream (no workgroup reads that row from the cache), and
 // attention covers L_b + 1 keys.
-// Loads of cache rows at or past L_b return zero (buffer range check, num_records = L_b rows),
-// so rows past the valid length are never read from memory.
+// Loads of cache rows at or past L_b return zero (buffer range check, num_records = L_b rows).
+// The one exception is each wave's first block, issued before L_b arrives from memory: it
+// reads within the cache allocation (N_max rows), and its rows at or past L_b are zeroed in
+// registers before use.  No value of a row at or past L_b reaches the result.
 //
 // Invalid lengths (L_b < 0 or L_b + append > N_max) cannot be rejected before launch (they
-// live in device memory): for such a batch row the kernel writes NaN to O and LSE, reads no
+// live in device memory): for such a batch row the kernel writes NaN to O and LSE, attends no
 // key and appends nothing.
 #include <hip/hip_runtime.h>
 
@@ -343,15 +345,25 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
 #pragma unroll
   for (int p = 0; p < kDP; ++p) pmask |= (uint32_t)(!Sh::kMaskD || 32 * p + 8 * c < D) << p;
 
-  const int Lc = seqlens ? seqlens[b] : N_max;  // valid cached rows
-  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
-  const int L = valid ? Lc + (append ? 1 : 0) : 0;  // keys attended
-  const int c0 = s * C;
-  const int c1 = min(c0 + C, L);
-
   T* Kh = Kc + b * ks.b + h * ks.h;
   T* Vh = Vc + b * vs.b + h * vs.h;
   const int krow = (int)ks.n * 2, vrow = (int)vs.n * 2;
+  const int k_lane = g * krow + 16 * c;
+  const int v_lane = g * vrow + 16 * c;
+  const int c0 = s * C;
+  int kb = c0 + wave * kWaveKeys;  // this wave's first block
+  // The first block's loads go out before the cache length arrives from memory: over the whole
+  // allocation (N_max rows, all addressable), with the rows at or past the length zeroed once
+  // it is known (below), so no stale or appended-row value reaches the sums.
+  KV<kDP> A;
+  if (kb < min(c0 + C, N_max))
+    load_block<Sh>(A, rows_rsrc(Kh, N_max * krow), rows_rsrc(Vh, N_max * vrow), krow, vrow, kb,
+                   true, k_lane, v_lane, pmask);
+
+  const int Lc = seqlens ? seqlens[b] : N_max;  // valid cached rows
+  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
+  const int L = valid ? Lc + (append ? 1 : 0) : 0;  // keys attended
+  const int c1 = min(c0 + C, L);
   const int Lr = valid ? Lc : 0;
   const __amdgpu_buffer_rsrc_t kd = rows_rsrc(Kh, Lr * krow);
   const __amdgpu_buffer_rsrc_t vd = rows_rsrc(Vh, Lr * vrow);
@@ -403,18 +415,22 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   // Cached rows of this chunk: [c0, ce).  The appended row (Lc, if it falls in this chunk) is
   // not read from the cache; wave 0 folds it in after the loop.
   const int ce = min(c1, Lc);
-  int kb = c0 + wave * kWaveKeys;
-  if (kb < ce) {
+  if (kb < ce) {  // then kb < min(c0 + C, N_max): A was loaded
     const int nblk = (ce - kb + kBlockKeys - 1) / kBlockKeys;  // this wave's blocks
-    const int k_lane = g * krow + 16 * c;
-    const int v_lane = g * vrow + 16 * c;
+#pragma unroll
+    for (int r = 0; r < kKeysPerLane; ++r)
+      if (kb + g + 16 * r >= Lr)
+#pragma unroll
+        for (int p = 0; p < kDP; ++p) {
+          A.k[r][p] = u32x4{0, 0, 0, 0};
+          A.v[r][p] = u32x4{0, 0, 0, 0};
+        }
     // Two register sets used in turn: the next block's loads are in flight while one block
     // is computed, with no copies between the sets (a copy would wait for the loads).  Pairs
     // of blocks per iteration, one back edge and no exit inside the body, so at the top of an
     // iteration only A's loads are outstanding.  (A third set was measured slower: the
     // compiler then waits for two sets before the first block of an iteration.)
-    KV<kDP> A, B;
-    load_block<Sh>(A, kd, vd, krow, vrow, kb, true, k_lane, v_lane, pmask);
+    KV<kDP> B;
     // The scheduling barriers keep each block's arithmetic after the loads issued before it:
     // left alone, the scheduler hoists the (independent) dot products of the next block, which
     // then wait for the loads just issued.
