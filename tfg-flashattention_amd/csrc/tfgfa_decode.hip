@@ -522,55 +522,68 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   }
 }
 
-// Combines the S partials of each head: one wave per head.  The lanes read the S partial
-// log-sum-exps in parallel (max and weight sum by wave reductions) and stage the weights
-// 2^(lse_s - M) in LDS; then each lane folds the S partial values of its head dims, four
-// independent loads at a time.  (A loop over the partials, one dependent load per split,
-// cost ~1 us per 4 splits.)
+// Combines the S partials of each head: one wave per head, lane = head dim (and head dim + 64).
+// The loads of a batch of kMergeBatch splits - every lane's partial values of those splits and
+// the splits' log-sum-exps - go out together, one memory round trip per batch (one in all for
+// S <= kMergeBatch); the weights 2^(lse_s - M) are formed in lanes 0..kMergeBatch-1 and read
+// back as scalars.  (Loops with one dependent load per split, or four at a time, cost 0.5-1.7
+// us more per graph-replayed step at the split shapes measured.)
 constexpr int kMaxSplits = 1024;
-template <class T>
+constexpr int kMergeBatch = 16;
+__device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t r, int off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+// kTwo: D > 64, every lane folds head dims lane and lane + 64.
+template <class T, bool kTwo>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float* __restrict__ part, const int* __restrict__ seqlens, T* __restrict__ O, Vecs os,
     float* __restrict__ LSE, int BH, int H, int N_max, int D, int S, bool append) {
-  __shared__ float sh_w[kMergeThreads / 64][kMaxSplits];
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR descriptors
   const int bh = blockIdx.x * (kMergeThreads / 64) + wave;
   if (bh >= BH) return;
   const int lane = threadIdx.x & 63;
   const int b = bh / H, h = bh - b * H;
   const int Lc = seqlens ? seqlens[b] : N_max;
   const int pstride = D + 1;
-  const float* p = part + (long long)bh * S * pstride;
-  float mx = -INFINITY;
-  for (int s = lane; s < S; s += 64) mx = fmaxf(mx, p[s * pstride + D]);
-  const float M = wave_max(mx);
-  const float M_use = (M == -INFINITY) ? 0.f : M;
-  float ws = 0.f;
-  for (int s = lane; s < S; s += 64) {
-    const float w = exp2f(p[s * pstride + D] - M_use);
-    sh_w[wave][s] = w;
-    ws += w;
-  }
-  const float wt = wave_sum(ws);
-  // The weights are read by other lanes of the same wave: the writes complete first, and the
-  // asm's memory clobber keeps the compiler from moving the reads above them.
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
-  for (int d = lane; d < D; d += 64) {
-    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-    int s = 0;
-    for (; s + 4 <= S; s += 4) {
-      const float x0 = p[s * pstride + d], x1 = p[(s + 1) * pstride + d];
-      const float x2 = p[(s + 2) * pstride + d], x3 = p[(s + 3) * pstride + d];
-      o0 = fmaf(sh_w[wave][s], x0, o0);
-      o1 = fmaf(sh_w[wave][s + 1], x1, o1);
-      o2 = fmaf(sh_w[wave][s + 2], x2, o2);
-      o3 = fmaf(sh_w[wave][s + 3], x3, o3);
+  // The head's S partials as one buffer: offsets past it read as zero.
+  const __amdgpu_buffer_rsrc_t pr = rows_rsrc(part + (long long)bh * S * pstride, S * pstride * 4);
+  const int js = lane & (kMergeBatch - 1);  // the split whose log-sum-exp this lane reads
+  float x0[kMergeBatch], x1[kMergeBatch], lse_j = -INFINITY;
+  auto load_batch = [&](int s0) {
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {
+      x0[j] = load_f32(pr, ((s0 + j) * pstride + lane) * 4);
+      x1[j] = kTwo ? load_f32(pr, ((s0 + j) * pstride + 64 + lane) * 4) : 0.f;
     }
-    for (; s < S; ++s) o0 = fmaf(sh_w[wave][s], p[s * pstride + d], o0);
-    const float ot = (o0 + o1) + (o2 + o3);
-    store_o<T>(O + b * os.b + h * os.h + d, wt > 0.f ? ot / wt : 0.f, valid);
+    const float v = load_f32(pr, ((s0 + js) * pstride + D) * 4);
+    lse_j = s0 + js < S ? v : -INFINITY;
+  };
+  float M;
+  if (S <= kMergeBatch) {
+    load_batch(0);
+    M = wave_max(lse_j);
+  } else {
+    float mx = -INFINITY;
+    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, load_f32(pr, (s * pstride + D) * 4));
+    M = wave_max(mx);
   }
+  const float M_use = (M == -INFINITY) ? 0.f : M;
+  float wt = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int s0 = 0; s0 < S; s0 += kMergeBatch) {
+    if (S > kMergeBatch) load_batch(s0);
+    const float w = exp2f(lse_j - M_use);  // 0 for splits past S
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {
+      const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+      wt += wj;
+      o0 = fmaf(wj, x0[j], o0);
+      if (kTwo) o1 = fmaf(wj, x1[j], o1);
+    }
+  }
+  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
+  T* orow = O + b * os.b + h * os.h;
+  if (lane < D) store_o<T>(orow + lane, wt > 0.f ? o0 / wt : 0.f, valid);
+  if (kTwo && lane + 64 < D) store_o<T>(orow + 64 + lane, wt > 0.f ? o1 / wt : 0.f, valid);
   if (LSE != nullptr && lane == 0)
     store_lse(LSE + bh, wt > 0.f ? (M + log2f(wt)) * kLn2 : -INFINITY, valid);
 }
@@ -728,10 +741,15 @@ static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
   if (e != hipSuccess) return -(int)e;
   if (S > 1) {
     const int heads_per_wg = kMergeThreads / 64;
-    hipLaunchKernelGGL(decode_merge_kernel<T>,
-                       dim3((unsigned)((bh + heads_per_wg - 1) / heads_per_wg)),
-                       dim3(kMergeThreads), 0, stream, static_cast<const float*>(workspace),
-                       cache_seqlens, ot, os, lse, (int)bh, H, N_max, D, S, append);
+    const dim3 mgrid((unsigned)((bh + heads_per_wg - 1) / heads_per_wg));
+    if (D > 64)
+      hipLaunchKernelGGL((decode_merge_kernel<T, true>), mgrid, dim3(kMergeThreads), 0, stream,
+                         static_cast<const float*>(workspace), cache_seqlens, ot, os, lse, (int)bh,
+                         H, N_max, D, S, append);
+    else
+      hipLaunchKernelGGL((decode_merge_kernel<T, false>), mgrid, dim3(kMergeThreads), 0, stream,
+                         static_cast<const float*>(workspace), cache_seqlens, ot, os, lse, (int)bh,
+                         H, N_max, D, S, append);
     e = hipGetLastError();
     if (e != hipSuccess) return -(int)e;
   }
