@@ -46,7 +46,7 @@ extern "C" {
 #define TFGFA_OK                 0
 #define TFGFA_ERR_NULL_POINTER   1  /* q, k, v or o is NULL                          */
 #define TFGFA_ERR_BAD_SHAPE      2  /* B, H or N negative                            */
-#define TFGFA_ERR_HEAD_DIM       3  /* D not a multiple of 8 in [8, 128] (not 64: *_bf16 entries) */
+#define TFGFA_ERR_HEAD_DIM       3  /* D not a multiple of 8 in [8, 128] (not 64: tfgfa_decode_bf16) */
 #define TFGFA_ERR_SCALE          4  /* softmax_scale not finite or not > 0           */
 #define TFGFA_ERR_CAUSAL_FLAG    5  /* causal is neither 0 nor 1                     */
 #define TFGFA_ERR_TOO_LARGE      6  /* grid or element count exceeds the limits      */
