@@ -117,6 +117,28 @@ def test_config_sampled_rows(name, nsample):
     assert np.all(np.abs(o) <= np.abs(v).max() + 1e-2)    # convex combination of V rows
 
 
+@pytest.mark.parametrize("dtype,N,D", [(torch.bfloat16, 65536, 64), (torch.float16, 32768, 128)])
+def test_long_sequences_sampled_rows(dtype, N, D):
+    """Sequences far past the configs (32-bit offset arithmetic, 512-1024 key tiles per
+    workgroup): sampled rows against the oracle, whole-tensor properties at full size."""
+    B, H = 1, 2
+    rnd = (lambda x: _bf(x)) if dtype == torch.bfloat16 else (lambda x: x.astype(np.float16).astype(np.float32))
+    q, k, v = (rnd(_rand((B, H, N, D), 5000 + N + D + i, 2.0 if i < 2 else 1.0)) for i in range(3))
+    _say(f"long sequence {dtype} N={N} D={D}")
+    qd, kd, vd = (torch.from_numpy(x).to(dtype).to(DEV) for x in (q, k, v))
+    o, lse = custom_flash_attn.attention(qd, kd, vd, return_lse=True)
+    torch.cuda.synchronize()
+    o, lse = o.float().cpu().numpy(), lse.cpu().numpy()
+    g = np.random.Generator(np.random.PCG64(N))
+    edges = [0, 1, 127, 128, N // 2 - 1, N // 2, N - 129, N - 128, N - 2, N - 1]
+    rows = np.unique(np.concatenate([edges, g.integers(0, N, 22)]))
+    o_ref, lse_ref = attention_c(q, k, v, 1.0 / math.sqrt(D), True, rows=rows)
+    _check(o[:, :, rows], lse[:, :, rows], o_ref, lse_ref, f"N={N} D={D}")
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
+    np.testing.assert_array_equal(o[:, :, 0], v[:, :, 0])  # row 0 attends only to key 0
+    assert np.all(np.abs(o) <= np.abs(v).max() + 1e-2)
+
+
 @pytest.mark.parametrize("name", ["config2", "config3", "config4"])
 def test_config_full_tensor_vs_reference_cpu_path(name):
     """Every output element of configs 2-4 against the reference's own CPU attention path
