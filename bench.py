@@ -299,6 +299,76 @@ def time_decode(dev, steps, warmup):
     }
 
 
+SPLIT_SHAPES = ((1, 25, 1024), (1, 16, 8192))  # (B, H, cache rows): one GPT-2-XL sequence, a long one
+
+
+def time_decode_split(dev, reps=20):
+    """Decode steps whose B*H leaves most CUs idle, so each head's cache is split over several
+    workgroups and a second kernel merges the partials: one GPT-2-XL sequence (B=1, H=25, a
+    1024-row cache) and a long context (B=1, H=16, 8192 rows).  bf16, d=64, every row valid, no
+    append; caches rotate through more than the Infinity Cache; steps replayed from a HIP graph
+    (no host gaps between the two launches of a step)."""
+    import torch
+
+    from custom_flash_attn import _C
+
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(4007)
+    stream = torch.cuda.current_stream(dev)
+    for (b, h, n) in SPLIT_SHAPES:
+        step_bytes = 2 * b * h * n * D * 2
+        nsets = max(2, -(-600_000_000 // step_bytes))
+        sets = [((torch.randn(b, h, n, D, device=dev, generator=gen) * SIGMA_QK).to(torch.bfloat16),
+                 torch.randn(b, h, n, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nsets)]
+        q = (torch.randn(b, h, D, device=dev, generator=gen) * SIGMA_QK).to(torch.bfloat16)
+        seqlens = torch.full((b,), n, dtype=torch.int32, device=dev)
+        o = torch.empty(b, h, D, device=dev, dtype=torch.bfloat16)
+        lse = torch.empty(b, h, device=dev, dtype=torch.float32)
+        ws_bytes = _C.decode_workspace_bytes(b, h, n)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        z3 = (0, 0, 0)
+
+        def step(i, sh):
+            kc, vc = sets[i % nsets]
+            _C.decode(q.data_ptr(), q.stride(), kc.data_ptr(), kc.stride(), vc.data_ptr(), vc.stride(),
+                      0, z3, 0, z3, seqlens.data_ptr(), o.data_ptr(), o.stride(), lse.data_ptr(),
+                      b, h, n, D, SCALE, ws.data_ptr(), ws_bytes, sh)
+
+        for i in range(2 * nsets):
+            step(i, stream.cuda_stream)
+        per_graph = 4 * nsets
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for i in range(per_graph):
+                    step(i, torch.cuda.current_stream(dev).cuda_stream)
+        stream.wait_stream(side)
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / (reps * per_graph)
+        algo = b * h * (2 * n * D * 2 + D * 2 + D * 2 + 4)
+        gbs = algo / (ms * 1e-3) / 1e9
+        out[f"B{b}_H{h}_L{n}"] = {
+            "ms_per_step_graph": round(ms, 5), "steps": reps * per_graph,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": algo},
+        }
+        del sets, graph
+    out["workload"] = ("decode step split over workgroups + merge kernel, bf16 d=64, all rows valid, "
+                       "caches rotating through HBM, HIP-graph replay")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -417,6 +487,7 @@ def main():
         result["strided_gpt2_views"] = time_strided_views(dev, max(1, args.steps // 2), max(1, args.warmup // 2))
     if not args.no_decode:
         result["decode"] = time_decode(dev, args.steps, args.warmup)
+        result["decode_split"] = time_decode_split(dev)
     if not args.no_generate:
         result["generate"] = time_generate(dev)
     if not args.no_cpu_baseline:

@@ -602,11 +602,15 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
 // rows 18.6 us with 2048-row splits -> 13.7 us; D = 128, 1 x 16 x 8192: 32.9 -> 21.3 us;
 // 1 x 8 x 2048: 14.1 -> 8.9 us.  Chunks are a multiple of kBlockKeys, no split is empty.
 constexpr int kSplitBytes = 64 * 1024;
+// Caches of fewer key blocks are not split: the merge kernel costs more than it saves there
+// (1 x 25 heads x 512 rows: 6.1 us as one workgroup per head, 7.6 us split; x 1024 rows: 8.5
+// against 7.9 us).
+constexpr int kMinSplitBlocks = 4;
 static void choose_split(int BH, int N_max, int D, int cu_count, int max_splits, int* S_out,
                          int* C_out) {
   const int blocks = std::max(1, (N_max + kBlockKeys - 1) / kBlockKeys);
   int S = 1;
-  if (2 * BH < cu_count) {
+  if (2 * BH < cu_count && blocks >= kMinSplitBlocks) {
     const int slots = cu_count * (D <= 64 ? 2 : 1);
     S = std::max(1, slots / BH);
     const int split_keys = std::max(kBlockKeys, kSplitBytes / (4 * D));
