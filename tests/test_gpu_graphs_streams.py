@@ -3,8 +3,9 @@
 The entry points allocate nothing and clear no memory with memsets, so a caller may capture
 them in a HIP graph.  Each graph below is replayed several times with eager work and
 synchronisations in between, and every replay is checked bitwise against the eager result of
-the same call (a replay that read stale or partial state would differ).  A second test runs
-different problems on two streams at once.
+the same call (a replay that read stale or partial state would differ); the decode step is
+replayed both as one kernel and as the split kernel plus its merge kernel.  Other tests run
+different forward and decode problems on two streams at once.
 """
 import sys
 
@@ -114,6 +115,77 @@ def test_decode_steps_replay_from_a_graph():
         assert torch.equal(seqlens, seqlens_ref)
         assert _same(kc, kc_ref) and _same(vc, vc_ref), f"step {t}: cache differs"
         assert _same(out, ref), f"step {t}: output differs"
+
+
+def test_split_decode_steps_replay_from_a_graph():
+    """Small B*H over a long cache: each step is the split decode kernel plus the merge kernel.
+    Both replay from one graph as the cache grows; every replay equals the eager step."""
+    B, H, N_max, D = 1, 4, 4096, 64
+    kc = torch.zeros(B, H, N_max, D, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    prefix = 3000
+    kc[:, :, :prefix] = _randn((B, H, prefix, D), 90, 3.0)
+    vc[:, :, :prefix] = _randn((B, H, prefix, D), 91)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    seqlens = torch.full((B,), prefix, dtype=torch.int32, device=DEV)
+    seqlens_ref = seqlens.clone()
+    q_in, kn_in, vn_in = (torch.empty(B, H, D, dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    out = torch.empty(B, H, D, dtype=torch.bfloat16, device=DEV)
+    lse = torch.empty(B, H, dtype=torch.float32, device=DEV)
+    ws = torch.empty(custom_flash_attn._C.decode_workspace_bytes(B, H, N_max), dtype=torch.uint8, device=DEV)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            o, l = custom_flash_attn.decode(q_in, kc, vc, seqlens, kn_in, vn_in, out=out, workspace=ws,
+                                            return_lse=True)
+            lse.copy_(l)
+            seqlens.add_(1)
+    torch.cuda.current_stream().wait_stream(side)
+    for t in range(4):
+        q, kn, vn = _randn((B, H, D), 100 + t, 3.0), _randn((B, H, D), 110 + t, 3.0), _randn((B, H, D), 120 + t)
+        q_in.copy_(q)
+        kn_in.copy_(kn)
+        vn_in.copy_(vn)
+        _ = (q.float() * 2).sum()  # eager work in between
+        torch.cuda.synchronize()
+        graph.replay()
+        ref, ref_lse = custom_flash_attn.decode(q, kc_ref, vc_ref, seqlens_ref, kn, vn, return_lse=True,
+                                                workspace=torch.empty_like(ws))
+        seqlens_ref.add_(1)
+        torch.cuda.synchronize()
+        _say(f"split decode graph replay {t}: length {prefix + t + 1}")
+        assert torch.equal(seqlens, seqlens_ref)
+        assert _same(kc, kc_ref) and _same(vc, vc_ref), f"step {t}: cache differs"
+        assert _same(out, ref) and torch.equal(lse, ref_lse), f"step {t}: output differs"
+
+
+def test_decode_on_two_streams_at_once():
+    """Decode calls with their own workspaces on two streams at once (split and unsplit
+    shapes) give the results of the same calls run one after the other."""
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    cases = []
+    for i, (B, H, N, D, dt) in enumerate([(1, 8, 4096, 64, torch.bfloat16), (8, 25, 1024, 64, torch.bfloat16),
+                                          (1, 16, 2048, 128, torch.float16)]):
+        kc = _randn((B, H, N, D), 130 + i, 3.0, dt)
+        vc = _randn((B, H, N, D), 140 + i, 1.0, dt)
+        q = _randn((B, H, D), 150 + i, 3.0, dt)
+        sl = torch.full((B,), N - 7, dtype=torch.int32, device=DEV)
+        ws = torch.empty(custom_flash_attn._C.decode_workspace_size(B, H, N, D), dtype=torch.uint8, device=DEV)
+        cases.append((q, kc, vc, sl, ws))
+    refs = [custom_flash_attn.decode(q, kc, vc, sl, workspace=ws) for q, kc, vc, sl, ws in cases]
+    torch.cuda.synchronize()
+    ws2 = [torch.empty_like(c[4]) for c in cases]
+    outs = []
+    for rep in range(3):
+        for i, (q, kc, vc, sl, ws) in enumerate(cases):
+            with torch.cuda.stream(s1 if (i + rep) % 2 == 0 else s2):
+                outs.append((i, custom_flash_attn.decode(q, kc, vc, sl, workspace=ws if rep % 2 == 0 else ws2[i])))
+    torch.cuda.synchronize()
+    for i, o in outs:
+        assert torch.equal(o.view(torch.int16), refs[i].view(torch.int16)), f"case {i} differs"
 
 
 def test_two_streams_at_once():
