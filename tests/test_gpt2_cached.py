@@ -55,6 +55,11 @@ def test_reference_generate_runs_on_cpu():
     with torch.no_grad():
         for t in range(7, 12):
             assert torch.equal(model(out[:, :t])[:, -1].argmax(-1), out[:, t])
+    # eos_id (model_inference.py:224-225), B = 1: stop before the first sampled eos_id.
+    one = out[:1]
+    eos = one[0, 9].item()
+    first = one[0, 7:].tolist().index(eos)
+    assert torch.equal(mi.generate(model, idx[:1], 5, 256, temperature=0.0, eos_id=eos), one[:, :7 + first])
 
 
 @pytest.mark.gpu
@@ -166,3 +171,30 @@ def test_graphed_decode_steps_match_eager_cached_steps():
     b = mi.generate_graphed(model, idx, 8, 256, temperature=0.0, decoder=dec)
     c = mi.generate_graphed(model, idx, 8, 256, temperature=0.0)
     assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.gpu
+def test_eos_id_stops_cached_and_graphed_generators_at_the_same_token():
+    """eos_id (model_inference.py:224-225): the loop stops before appending the first sampled
+    token equal to eos_id.  Greedy, B = 1: the cached and graph-replayed generators stop where
+    a run without eos_id first produces that token, and return the same prefix; an eos_id never
+    produced leaves the full length."""
+    torch.manual_seed(0)
+    cfg = _small_cfg("hip")
+    model = mi.GPTModel(cfg).eval().to("cuda:0")
+    mi.init_gpt2_weights(model, SEED_W)
+    P, T = 10, 12
+    idx = torch.randint(0, cfg["vocab_size"], (1, P), generator=torch.Generator().manual_seed(21)).to("cuda:0")
+    full = mi.generate_cached(model, idx, T, 256, temperature=0.0)
+    assert full.shape == (1, P + T)
+    new = full[0, P:].tolist()
+    eos = new[T // 2]
+    first = new.index(eos)
+    _say(f"greedy tokens {new}; eos_id {eos} first sampled at step {first}")
+    expect = full[:, :P + first]
+    a = mi.generate_cached(model, idx, T, 256, temperature=0.0, eos_id=eos)
+    b = mi.generate_graphed(model, idx, T, 256, temperature=0.0, eos_id=eos)
+    assert torch.equal(a, expect) and torch.equal(b, expect)
+    absent = next(t for t in range(cfg["vocab_size"]) if t not in new)
+    c = mi.generate_graphed(model, idx, T, 256, temperature=0.0, eos_id=absent)
+    assert torch.equal(c, full)
