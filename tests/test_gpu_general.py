@@ -146,3 +146,32 @@ def test_bf16_d64_general_path_equals_forward():
     b = custom_flash_attn.forward(q, k, v)
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("D", [64, 128, 40])
+@pytest.mark.parametrize("layout", ["contiguous", "projection views"])
+@pytest.mark.parametrize("nq,nk,causal", [(1024, 1024, True), (300, 520, False), (97, 97, True)])
+def test_o_only_call_equals_o_of_the_lse_call(dt, D, layout, nq, nk, causal):
+    """Without an LSE output the kernel does not keep the fp32 probability sum the LSE needs.
+    O is normalised by the other sum (of the rounded probabilities) in both cases, so O is
+    bitwise the same with and without the LSE, for every instance (dense GPT-2 layout,
+    strided, head dims below the compiled ones)."""
+    dtype = DTYPES[dt]
+    B, H = 2, 3
+    if layout == "contiguous":
+        q, qn = _rand((B, H, nq, D), 40 + D + nq, dtype, 3.0)
+        k, kn = _rand((B, H, nk, D), 41 + D + nk, dtype, 3.0)
+        v, vn = _rand((B, H, nk, D), 42 + D, dtype)
+    else:
+        x, _ = _rand((B, nq, 3, H, D), 43 + D + nq, dtype, 3.0)
+        y, _ = _rand((B, nk, 2, H, D), 44 + D + nk, dtype, 2.0)
+        q = x[:, :, 0].transpose(1, 2)
+        k, v = y[:, :, 0].transpose(1, 2), y[:, :, 1].transpose(1, 2)
+    o_only = custom_flash_attn.attention(q, k, v, causal=causal)
+    o, lse = custom_flash_attn.attention(q, k, v, causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_only.view(torch.int16), o.view(torch.int16)), f"{dt} D={D} {layout}"
+    if layout == "contiguous" and nq == 97:
+        o_ref, l_ref = attention_c(qn, kn, vn, 1.0 / math.sqrt(D), causal)
+        _check(o_only, lse, o_ref, l_ref, f"O only, {dt} D={D}")

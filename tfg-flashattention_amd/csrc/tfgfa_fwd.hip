@@ -208,10 +208,12 @@ __device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
 
 // Compile-time shape of one kernel instance: head dims kD (64 or 128, = kDH dim halves of 64),
 // element type T, and kMaskD: the actual head dim D may be below kD (a multiple of 8); 16-B
-// chunks of dims >= D load zeros and are not stored.
-template <int kD_, typename T_, bool kMaskD_>
+// chunks of dims >= D load zeros and are not stored.  kLse: the LSE is written, so the fp32
+// sum l_run is kept (without it only l_p, which normalises O, is summed).
+template <int kD_, typename T_, bool kMaskD_, bool kLse_ = true>
 struct Shape {
   static constexpr int kD = kD_;
+  static constexpr bool kLse = kLse_;
   static constexpr int kDH = kD_ / kDHalf;
   static constexpr bool kMaskD = kMaskD_;
   typedef T_ T;
@@ -363,7 +365,7 @@ __device__ __forceinline__ void move_offset(WaveState<Sh>& w, float mx, float sc
     const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
     w.m_run = m_new;
     w.thr = (m_new + Elem<typename Sh::T>::kMargin) * inv_scale_log2;
-    w.l_run *= alpha;
+    if constexpr (Sh::kLse) w.l_run *= alpha;
     w.l_p *= alpha;
 #pragma unroll
     for (int i = 0; i < 2 * Sh::kDH; ++i)
@@ -378,13 +380,15 @@ __device__ __forceinline__ void move_offset(WaveState<Sh>& w, float mx, float sc
 template <class Sh, class P>
 __device__ __forceinline__ void sum_convert(WaveState<Sh>& w, const P& p) {
   typedef typename Sh::T T;
-  float ps0 = p[0], ps1 = p[1];
+  if constexpr (Sh::kLse) {
+    float ps0 = p[0], ps1 = p[1];
 #pragma unroll
-  for (int t = 2; t < 16; t += 2) {
-    ps0 += p[t];
-    ps1 += p[t + 1];
+    for (int t = 2; t < 16; t += 2) {
+      ps0 += p[t];
+      ps1 += p[t + 1];
+    }
+    w.l_run += ps0 + ps1;
   }
-  w.l_run += ps0 + ps1;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     w.pb[0][e] = (T)p[e];
@@ -474,7 +478,7 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
     const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
     w.m_run = m_new;
     w.thr = (m_new + Elem<typename Sh::T>::kMargin) * inv_scale_log2;
-    w.l_run *= alpha;
+    if constexpr (Sh::kLse) w.l_run *= alpha;
     w.l_p *= alpha;
 #pragma unroll
     for (int i = 0; i < 2 * Sh::kDH; ++i)
@@ -487,11 +491,12 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
 #pragma unroll
   for (int t = 0; t < 16; ++t) acc[t] = 0.f;
   float ps0 = 0.f, ps1 = 0.f;
+  constexpr int kConvChunk = Sh::kLse ? 1 : 0;  // chunk 0 sums l_run when there is one
 #pragma unroll
   for (int i = 0; i < kS; ++i) {
     acc = Elem<T>::mfma(kop[i & 1], w.qop[i], acc);
     if (i + 2 < kS) kop[i & 1] = k_operand<Sh, kKs, kKh>(w, lds, i + 2);
-    if (i == 0) {
+    if (i == 0 && Sh::kLse) {
       ps0 = p[0];
       ps1 = p[1];
 #pragma unroll
@@ -501,14 +506,14 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
       }
       w.l_run += ps0 + ps1;
       asm volatile("" : "+v"(w.l_run));
-    } else if (i == 1) {
+    } else if (i == kConvChunk) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         w.pb[0][e] = (T)p[e];
         w.pb[1][e] = (T)p[8 + e];
       }
       asm volatile("" : "+v"(w.pb[0]), "+v"(w.pb[1]));
-    } else if (i == 2) {
+    } else if (i == kConvChunk + 1) {
       w.l_p = Elem<T>::sum8(w.pb[1], Elem<T>::sum8(w.pb[0], w.l_p));
       asm volatile("" : "+v"(w.l_p));
     }
@@ -793,7 +798,7 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
 
   // Row sums over the lane pair (both lanes of a row hold the same offset).
   const float l_o = pair_sum(w.l_p);
-  const float l_all = pair_sum(w.l_run);
+  const float l_all = Sh::kLse ? pair_sum(w.l_run) : 0.f;
   if (qrow < Nq) {
     const float inv_l = 1.0f / l_o;
     T* orow = kDense ? O + dense_head + (long long)qrow * Sh::kD
@@ -809,7 +814,7 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
         for (int r = 0; r < 4; ++r) x[r] = (T)(w.o[i][4 * g + r] * inv_l);
         if (!Sh::kMaskD || d0 < D) *reinterpret_cast<v4*>(orow + d0) = x;
       }
-    if (LSE != nullptr && h == 0) {
+    if (Sh::kLse && LSE != nullptr && h == 0) {
       LSE[(size_t)bh * Nq + qrow] = (w.m_run + __builtin_amdgcn_logf(l_all)) * kLn2;
     }
   }
@@ -935,12 +940,18 @@ static void launch_dims(const LaunchArgs& a, bool dense, hipStream_t stream) {
     return;
   }
   if constexpr (kD == 64 && std::is_same<T, __bf16>::value) {
-    if (dense) {
-      launch_instance<Shape<kD, T, false>, true>(a, stream);  // the GPT-2 layout
+    if (dense) {  // the GPT-2 layout
+      if (a.lse != nullptr)
+        launch_instance<Shape<kD, T, false>, true>(a, stream);
+      else
+        launch_instance<Shape<kD, T, false, false>, true>(a, stream);
       return;
     }
   }
-  launch_instance<Shape<kD, T, false>, false>(a, stream);
+  if (a.lse != nullptr)
+    launch_instance<Shape<kD, T, false>, false>(a, stream);
+  else
+    launch_instance<Shape<kD, T, false, false>, false>(a, stream);
 }
 
 static int launch(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
