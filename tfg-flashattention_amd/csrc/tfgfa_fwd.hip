@@ -120,6 +120,9 @@ struct Elem<__bf16> {
   }
   // Offset margin (log2 units): P <= 2^64 keeps the fp32 sums finite for |V| * N < 2^64.
   static constexpr float kMargin = 64.0f;
+  // Bound on a half's probability sum in the fused half-step's offset check (every P of the
+  // half is at most the sum): the margin's bound.
+  static constexpr float kSumBound = 0x1p64f;
   // acc + the sum of the 8 elements of p (exact products by 1, fp32 accumulation).
   static __device__ __forceinline__ float sum8(v8 p, float acc) {
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -140,6 +143,8 @@ struct Elem<_Float16> {
   }
   // P <= 2^15 stays inside fp16's range (65504).
   static constexpr float kMargin = 15.0f;
+  // The sum check only needs every P of the half finite in fp16: at most 65504.
+  static constexpr float kSumBound = 65504.0f;
   static __device__ __forceinline__ float sum8(v8 p, float acc) {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
@@ -433,14 +438,17 @@ __device__ __forceinline__ typename Elem<typename Sh::T>::v8 k_operand(const Wav
 
 // A full half-step u as a fixed sequence of chunks, each MFMA followed by a share of the VALU
 // work that does not depend on it (a wave's VALU work overlaps its own in-flight MFMAs):
-//   chunk 0          V^T operands of the first two P.V MFMAs; lane max of S_u and the
-//                    offset check
+//   chunk 0          V^T operands of the first two P.V MFMAs
 //   chunks 1..kPv    MFMA i of O += V_{u-1} P_{u-1}, the next operand read, a share of
 //                    P_u = exp2(scale*log2e*S_u - m_run)
-//   (rare branch)    move the offset: rescale O and the sums, recompute P_u (the chunks'
-//                    exps stay in their chunks: each is pinned there by an empty asm)
 //   chunks kPv+1..   MFMA i of S_{u+1} = K_{u+1} Q^T, the next operand read, a share of
 //                    the sums of P_u and its conversion to the element type
+// The offset check reads the sum of the half's probabilities as rounded to the element type:
+// a rounded P above the type's bound (2^64 for bf16, fp16's largest finite value) makes that
+// sum exceed it (an overflow gives +inf, a -inf offset on a wave's first half gives +inf or
+// NaN), so a sum above the bound, or not a number, takes the rare branch: move the offset to
+// the rows' exact running max, rescale O and the sums, recompute P_u.  A sum above the bound
+// without any single P above it moves the offset early, which is harmless.
 template <class Sh, int kVs, int kVh, int kKs, int kKh>
 __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, float scale_log2,
                                            float inv_scale_log2) {
@@ -448,11 +456,10 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
   typedef typename Elem<T>::v8 v8;
   constexpr int kPv = 4 * Sh::kDH;
   constexpr int kS = 4 * Sh::kDH;
+  constexpr float kSumBound = Elem<T>::kSumBound;
   v8 vop[2];
   vop[0] = v_operand<Sh, kVs, kVh>(w, lds, 0);
   vop[1] = v_operand<Sh, kVs, kVh>(w, lds, 1);
-  const float mx = lane_max(w);
-  const bool move = __builtin_amdgcn_ballot_w64(mx > w.thr) != 0;
   TFGFA_FENCE();
   const float neg_m = -w.m_run;
   float p[16];
@@ -468,54 +475,64 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
 #pragma unroll
     for (int t = 16 * i / kPv; t < 16 * (i + 1) / kPv; ++t)
       p[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, neg_m));
-    // Computed here, in this chunk, even though the rare branch below recomputes them.
+    // Computed here, in this chunk, even though the rare branch recomputes them.
 #pragma unroll
     for (int t = 16 * i / kPv; t < 16 * (i + 1) / kPv; ++t) asm volatile("" : "+v"(p[t]));
     TFGFA_FENCE();
   }
-  if (move) {
-    const float m_new = fmaxf(w.m_run, pair_max(mx) * scale_log2);
-    const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
-    w.m_run = m_new;
-    w.thr = (m_new + Elem<typename Sh::T>::kMargin) * inv_scale_log2;
-    if constexpr (Sh::kLse) w.l_run *= alpha;
-    w.l_p *= alpha;
-#pragma unroll
-    for (int i = 0; i < 2 * Sh::kDH; ++i)
-#pragma unroll
-      for (int t = 0; t < 16; ++t) w.o[i][t] *= alpha;
-#pragma unroll
-    for (int t = 0; t < 16; ++t) p[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, -m_new));
-  }
   f32x16 acc;
 #pragma unroll
   for (int t = 0; t < 16; ++t) acc[t] = 0.f;
-  float ps0 = 0.f, ps1 = 0.f;
-  constexpr int kConvChunk = Sh::kLse ? 1 : 0;  // chunk 0 sums l_run when there is one
+  // Chunk 0 converts P_u to the element type, chunk 1 sums the rounded values, checks the
+  // offset on that sum and adds it to l_p, chunk 2 adds the fp32 sum to l_run (LSE only).  Both
+  // instances (with and without the LSE) take the same branch decisions, so their O agree bit
+  // for bit.
+  auto convert = [&w](const float* q) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      w.pb[0][e] = (T)q[e];
+      w.pb[1][e] = (T)q[8 + e];
+    }
+  };
 #pragma unroll
   for (int i = 0; i < kS; ++i) {
     acc = Elem<T>::mfma(kop[i & 1], w.qop[i], acc);
     if (i + 2 < kS) kop[i & 1] = k_operand<Sh, kKs, kKh>(w, lds, i + 2);
-    if (i == 0 && Sh::kLse) {
-      ps0 = p[0];
-      ps1 = p[1];
+    if (i == 0) {
+      convert(p);
+      asm volatile("" : "+v"(w.pb[0]), "+v"(w.pb[1]));
+    } else if (i == 1) {
+      float hs = Elem<T>::sum8(w.pb[1], Elem<T>::sum8(w.pb[0], 0.f));
+      // As unsigned integers, the bits of a sum >= +0 exceed those of the bound exactly when
+      // the sum does, is +inf or is a NaN (the device pass assumes no NaN in float compares).
+      if (__builtin_amdgcn_ballot_w64(__float_as_uint(hs) > __float_as_uint(kSumBound)) != 0) {
+        const float mx = lane_max(w);
+        const float m_new = fmaxf(w.m_run, pair_max(mx) * scale_log2);
+        const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
+        w.m_run = m_new;
+        w.thr = (m_new + Elem<T>::kMargin) * inv_scale_log2;
+        if constexpr (Sh::kLse) w.l_run *= alpha;
+        w.l_p *= alpha;
+#pragma unroll
+        for (int j = 0; j < 2 * Sh::kDH; ++j)
+#pragma unroll
+          for (int t = 0; t < 16; ++t) w.o[j][t] *= alpha;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) p[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, -m_new));
+        convert(p);
+        hs = Elem<T>::sum8(w.pb[1], Elem<T>::sum8(w.pb[0], 0.f));
+      }
+      w.l_p += hs;
+      asm volatile("" : "+v"(w.l_p));
+    } else if (i == 2 && Sh::kLse) {
+      float s0 = p[0], s1 = p[1];
 #pragma unroll
       for (int t = 2; t < 16; t += 2) {
-        ps0 += p[t];
-        ps1 += p[t + 1];
+        s0 += p[t];
+        s1 += p[t + 1];
       }
-      w.l_run += ps0 + ps1;
+      w.l_run += s0 + s1;
       asm volatile("" : "+v"(w.l_run));
-    } else if (i == kConvChunk) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        w.pb[0][e] = (T)p[e];
-        w.pb[1][e] = (T)p[8 + e];
-      }
-      asm volatile("" : "+v"(w.pb[0]), "+v"(w.pb[1]));
-    } else if (i == kConvChunk + 1) {
-      w.l_p = Elem<T>::sum8(w.pb[1], Elem<T>::sum8(w.pb[0], w.l_p));
-      asm volatile("" : "+v"(w.l_p));
     }
     TFGFA_FENCE();
   }
