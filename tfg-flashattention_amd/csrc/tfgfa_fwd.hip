@@ -816,23 +816,28 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   // Row sums over the lane pair (both lanes of a row hold the same offset).
   const float l_o = pair_sum(w.l_p);
   const float l_all = Sh::kLse ? pair_sum(w.l_run) : 0.f;
-  if (qrow < Nq) {
+  // The lane's row again, from the lane id (mbcnt) rather than a value kept from the prologue:
+  // a register held across the loops for the epilogue only was spilled to scratch.
+  int lane_e;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
+  const int qrow_e = q0 + (lane_e & 31), h_e = lane_e >> 5;
+  if (qrow_e < Nq) {
     const float inv_l = 1.0f / l_o;
-    T* orow = kDense ? O + dense_head + (long long)qrow * Sh::kD
-                     : O + bb * os.b + hh * os.h + (long long)qrow * os.n;
+    T* orow = kDense ? O + dense_head + (long long)qrow_e * Sh::kD
+                     : O + bb * os.b + hh * os.h + (long long)qrow_e * os.n;
 #pragma unroll
     for (int i = 0; i < 2 * Sh::kDH; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         // Register 4g + r of tile i holds dim 32i + 8g + 4h + r.
-        const int d0 = 32 * i + 8 * g + 4 * h;
+        const int d0 = 32 * i + 8 * g + 4 * h_e;
         v4 x;
 #pragma unroll
         for (int r = 0; r < 4; ++r) x[r] = (T)(w.o[i][4 * g + r] * inv_l);
         if (!Sh::kMaskD || d0 < D) *reinterpret_cast<v4*>(orow + d0) = x;
       }
-    if (Sh::kLse && LSE != nullptr && h == 0) {
-      LSE[(size_t)bh * Nq + qrow] = (w.m_run + __builtin_amdgcn_logf(l_all)) * kLn2;
+    if (Sh::kLse && LSE != nullptr && h_e == 0) {
+      LSE[(size_t)bh * Nq + qrow_e] = (w.m_run + __builtin_amdgcn_logf(l_all)) * kLn2;
     }
   }
 }
