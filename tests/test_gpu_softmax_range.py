@@ -1,8 +1,9 @@
 """The forward's softmax over extreme score patterns (GPU box only).
 
-The kernel keeps a per-row exp2 offset that moves only when a score passes it by a margin (64
-log2 units for bf16, 15 for fp16); a move rescales O and both sums and recomputes the half's
-probabilities.  Random inputs at the configs' scales move it about once per row, so these
+The kernel keeps a per-row exp2 offset that moves only when a lane's probabilities of a half,
+as rounded for the MFMA, sum past a bound (2^64 for bf16, 65504 for fp16), or, on a wave's last
+half, when a score passes it by a margin (64 log2 units for bf16, 15 for fp16); a move rescales
+O and both sums and recomputes the half's probabilities.  Random inputs at the configs' scales move it about once per row, so these
 cases force the other paths: scores that climb by far more than the margin every half (a move
 on every half, with rescale factors that underflow to 0), scores that fall (no move after the
 first half), halves that alternate high and low, and scores of magnitude ~1e4 (one-hot rows).
@@ -69,7 +70,9 @@ def test_extreme_score_patterns(kind, N, D, dtype):
     qd, kd, vd = (torch.from_numpy(x).to(t).to(DEV) for x in (q, k, v))
     scale = 1.0 / math.sqrt(D)
     o, lse = custom_flash_attn.attention(qd, kd, vd, return_lse=True)
+    o_only = custom_flash_attn.attention(qd, kd, vd)  # the instance without the LSE's sum
     torch.cuda.synchronize()
+    assert torch.equal(o_only.view(torch.int16), o.view(torch.int16)), "O-only call differs"
     o_ref, l_ref = attention_np(q, k, v, scale, True)
     o = o.float().cpu().numpy().astype(np.float64)
     lse = lse.cpu().numpy().astype(np.float64)
