@@ -69,9 +69,12 @@ extern "C" {
  * batch_size, num_heads) (src/cpp/v1.cu:4-38, instantiated :40-42), whose
  * scale is fixed to 1/sqrt(64) (v1.cu:16) and whose launch goes to the legacy
  * default stream (v1.cu:33-34).  D: a multiple of 8 up to 128 (the reference
- * compiles 64 only, common_types.hpp:33); tfgfa_fwd with dtype bf16, N_q = N_k.  Here the scale is explicit (pass 0.125 for
- * the reference's behaviour), `lse` may be NULL, and `hip_stream` (a
- * hipStream_t, NULL = default stream) is the stream the caller is using.
+ * compiles 64 only, common_types.hpp:33); tfgfa_fwd with dtype bf16,
+ * N_q = N_k.  Here the scale is explicit (pass 0.125 for the reference's
+ * behaviour), `lse` may be NULL (the reference's O-only call; a kernel built
+ * without the LSE's running sum then runs, O bitwise the same), and
+ * `hip_stream` (a hipStream_t, NULL = default stream) is the stream the
+ * caller is using.
  * B, H or N equal to 0 is an empty problem: nothing is launched and 0 is returned,
  * whatever the pointers are (an empty torch tensor's data pointer is NULL).
  */
