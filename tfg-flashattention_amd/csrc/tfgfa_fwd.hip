@@ -502,7 +502,7 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
       convert(p);
       asm volatile("" : "+v"(w.pb[0]), "+v"(w.pb[1]));
     } else if (i == 1) {
-      float hs = Elem<T>::sum8(w.pb[1], Elem<T>::sum8(w.pb[0], 0.f));
+      float hs = Elem<T>::sum8(w.pb[0], 0.f) + Elem<T>::sum8(w.pb[1], 0.f);
       // As unsigned integers, the bits of a sum >= +0 exceed those of the bound exactly when
       // the sum does, is +inf or is a NaN (the device pass assumes no NaN in float compares).
       if (__builtin_amdgcn_ballot_w64(__float_as_uint(hs) > __float_as_uint(kSumBound)) != 0) {
@@ -520,7 +520,7 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
 #pragma unroll
         for (int t = 0; t < 16; ++t) p[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, -m_new));
         convert(p);
-        hs = Elem<T>::sum8(w.pb[1], Elem<T>::sum8(w.pb[0], 0.f));
+        hs = Elem<T>::sum8(w.pb[0], 0.f) + Elem<T>::sum8(w.pb[1], 0.f);
       }
       w.l_p += hs;
       asm volatile("" : "+v"(w.l_p));
