@@ -99,10 +99,13 @@ constexpr int kMaxD = 128;
 constexpr int kOutOfRange = 0x7FFFFFF0;
 
 // The exp2 offset m of a row moves (to the row's exact running max, rescaling O and the sums)
-// only when some score exceeds it by more than the element type's margin (log2 units), so
-// P <= 2^margin and the rescale is rare.  O is normalised by l_p, the sum of the probabilities
-// *as rounded* for the P.V MFMA, so the rounding of a dominant probability cancels between O's
-// numerator and denominator; the LSE uses l_run, the fp32 sum of the unrounded ones.
+// only when the probabilities grow too large: in a full half-step, when a lane's sum of its
+// rounded probabilities passes the element type's bound (2^64 bf16, 65504 fp16); in a wave's
+// last half-step, when some score exceeds m by more than the type's margin (64 / 15 log2
+// units).  So P stays bounded and the rescale is rare.  O is normalised by l_p, the sum of the
+// probabilities *as rounded* for the P.V MFMA, so the rounding of a dominant probability
+// cancels between O's numerator and denominator; the LSE uses l_run, the fp32 sum of the
+// unrounded ones.
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
