@@ -1,12 +1,13 @@
 """The forward's softmax over extreme score patterns (GPU box only).
 
-The kernel keeps a per-row exp2 offset that moves only when a lane's probabilities of a half,
-as rounded for the MFMA, sum past a bound (2^64 for bf16, 65504 for fp16), or, on a wave's last
-half, when a score passes it by a margin (64 log2 units for bf16, 15 for fp16); a move rescales
-O and both sums and recomputes the half's probabilities.  Random inputs at the configs' scales move it about once per row, so these
-cases force the other paths: scores that climb by far more than the margin every half (a move
-on every half, with rescale factors that underflow to 0), scores that fall (no move after the
-first half), halves that alternate high and low, and scores of magnitude ~1e4 (one-hot rows).
+The kernel keeps a per-row exp2 offset that moves only when (bf16) a lane's probabilities of a
+half, as rounded for the MFMA, sum past 2^64, or (fp16, and a wave's last half) when a score
+passes it by a margin (64 log2 units for bf16, 15 for fp16); a move rescales O and both sums
+and recomputes the half's probabilities.  Random inputs at the configs' scales move it about
+once per row, so these cases force the other paths: scores that climb by far more than the
+margin every half (a move on every half, with rescale factors that underflow to 0), scores
+that fall (no move after the first half), halves that alternate high and low, and scores of
+magnitude ~1e4 (one-hot rows).
 
 Oracle: attention_np (fp64, tests/test_oracle.py) on the same bf16/fp16-rounded inputs.
 Tolerances as everywhere: max|dO| <= 2e-2, mean|dO| <= 2e-3; LSE within 1e-3 plus the fp32

@@ -99,10 +99,9 @@ constexpr int kMaxD = 128;
 constexpr int kOutOfRange = 0x7FFFFFF0;
 
 // The exp2 offset m of a row moves (to the row's exact running max, rescaling O and the sums)
-// only when the probabilities grow too large: in a full half-step, when a lane's sum of its
-// rounded probabilities passes the element type's bound (2^64 bf16, 65504 fp16); in a wave's
-// last half-step, when some score exceeds m by more than the type's margin (64 / 15 log2
-// units).  So P stays bounded and the rescale is rare.  O is normalised by l_p, the sum of the
+// only when the probabilities grow too large: for bf16 in a full half-step, when a lane's sum
+// of its rounded probabilities passes 2^64; otherwise (fp16, and a wave's last half-step),
+// when some score exceeds m by more than the type's margin (64 / 15 log2 units).  So P stays bounded and the rescale is rare.  O is normalised by l_p, the sum of the
 // probabilities *as rounded* for the P.V MFMA, so the rounding of a dominant probability
 // cancels between O's numerator and denominator; the LSE uses l_run, the fp32 sum of the
 // unrounded ones.
@@ -146,7 +145,8 @@ struct Elem<_Float16> {
   }
   // P <= 2^15 stays inside fp16's range (65504).
   static constexpr float kMargin = 15.0f;
-  // The sum check only needs every P of the half finite in fp16: at most 65504.
+  // What a sum check would need (every rounded P finite in fp16); the fp16 instances use the
+  // lane-max check instead, which moves the offset less often at this bound.
   static constexpr float kSumBound = 65504.0f;
   static __device__ __forceinline__ float sum8(v8 p, float acc) {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -446,12 +446,13 @@ __device__ __forceinline__ typename Elem<typename Sh::T>::v8 k_operand(const Wav
 //                    P_u = exp2(scale*log2e*S_u - m_run)
 //   chunks kPv+1..   MFMA i of S_{u+1} = K_{u+1} Q^T, the next operand read, a share of
 //                    the sums of P_u and its conversion to the element type
-// The offset check reads the sum of the half's probabilities as rounded to the element type:
-// a rounded P above the type's bound (2^64 for bf16, fp16's largest finite value) makes that
-// sum exceed it (an overflow gives +inf, a -inf offset on a wave's first half gives +inf or
-// NaN), so a sum above the bound, or not a number, takes the rare branch: move the offset to
-// the rows' exact running max, rescale O and the sums, recompute P_u.  A sum above the bound
-// without any single P above it moves the offset early, which is harmless.
+// The offset check (bf16) reads the sum of the half's probabilities as rounded to the element
+// type: a rounded P above 2^64 makes that sum exceed it (an overflow gives +inf, a -inf offset
+// on a wave's first half gives +inf or NaN), so a sum above the bound, or not a number, takes
+// the rare branch: move the offset to the rows' exact running max, rescale O and the sums,
+// recompute P_u.  A sum above the bound without any single P above it moves the offset early,
+// which is harmless.  fp16 checks the lane max of the scores against the margin instead, in
+// chunk 0, and takes the same branch.
 template <class Sh, int kVs, int kVh, int kKs, int kKh>
 __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, float scale_log2,
                                            float inv_scale_log2) {
@@ -463,6 +464,15 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
   v8 vop[2];
   vop[0] = v_operand<Sh, kVs, kVh>(w, lds, 0);
   vop[1] = v_operand<Sh, kVs, kVh>(w, lds, 1);
+  // fp16 keeps the lane-max check (a score more than the margin above the offset): its sum
+  // bound is tight enough that the sum check moved the offset more often.
+  constexpr bool kMaxCheck = std::is_same<T, _Float16>::value;
+  float mx = 0.f;
+  bool max_move = false;
+  if constexpr (kMaxCheck) {
+    mx = lane_max(w);
+    max_move = __builtin_amdgcn_ballot_w64(mx > w.thr) != 0;
+  }
   TFGFA_FENCE();
   const float neg_m = -w.m_run;
   float p[16];
@@ -508,8 +518,10 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
       float hs = Elem<T>::sum8(w.pb[0], 0.f) + Elem<T>::sum8(w.pb[1], 0.f);
       // As unsigned integers, the bits of a sum >= +0 exceed those of the bound exactly when
       // the sum does, is +inf or is a NaN (the device pass assumes no NaN in float compares).
-      if (__builtin_amdgcn_ballot_w64(__float_as_uint(hs) > __float_as_uint(kSumBound)) != 0) {
-        const float mx = lane_max(w);
+      const bool move = kMaxCheck ? max_move
+                        : __builtin_amdgcn_ballot_w64(__float_as_uint(hs) > __float_as_uint(kSumBound)) != 0;
+      if (move) {
+        if constexpr (!kMaxCheck) mx = lane_max(w);
         const float m_new = fmaxf(w.m_run, pair_max(mx) * scale_log2);
         const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
         w.m_run = m_new;
