@@ -8,12 +8,15 @@ already resident in HBM; four input sets are rotated so the 105 MB working set o
 call does not stay in the 256 MB Infinity Cache from one step to the next.
 
 Prints one JSON line.  ``value`` is TFLOP/s with the FlashAttention causal convention
-(4*B*H*N^2*d/2 FLOPs per forward).  ``roofline`` compares it with the dense bf16 MFMA peak;
-``cpu_baseline`` times the reference's PyTorch CPU attention path (the "manual" branch of
-src/py/model_inference.py:68-75) on this host's cores.
+(4*B*H*N^2*d/2 FLOPs per forward), from the K timed steps bracketed by synchronisations.
+``roofline`` compares it with the dense bf16 MFMA peak; ``cpu_baseline`` times the
+reference's PyTorch CPU attention path (the "manual" branch of src/py/model_inference.py:68-75)
+on this host's cores.  ``configs`` times every BASELINE.json attention config (1-4, plus the
+drop-in O-only call at config 3) by per-launch events: the median of at least 200 launches
+after a warm-up of at least 0.1 s, whatever --steps and --warmup say.
 
 Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 2000] [--no-cpu-baseline] [--no-strided]
-                      [--no-decode] [--no-generate]
+                      [--no-decode] [--no-generate] [--no-configs]
 """
 import argparse
 import json
@@ -34,6 +37,74 @@ SCALE = 1.0 / math.sqrt(D)
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (published)
 PEAK_HBM_GBS = 8000.0
 N_SETS = 4
+WARM_S = 0.1        # launches before any timing: clocks settle within ~0.1 s of back-to-back work
+MIN_PER_CALL = 200  # per-launch timings behind every median
+
+
+def _warm(step, seconds=WARM_S, min_calls=10):
+    """Launches ``step(i)`` back to back until at least ``seconds`` of GPU time have passed
+    (and at least ``min_calls`` launches); returns the number of launches."""
+    import torch
+
+    n, t0 = 0, time.perf_counter()
+    while True:
+        for _ in range(8):
+            step(n)
+            n += 1
+        torch.cuda.synchronize()
+        if n >= min_calls and time.perf_counter() - t0 >= seconds:
+            return n
+
+
+def _per_call_ms(step, stream, calls=MIN_PER_CALL, group=10):
+    """Median and mean per-launch time of ``calls`` launches of ``step(i)``, run back to back in
+    groups of ``group`` launches between two events on the launch stream: the median is taken
+    over the groups' per-launch averages (events around every single launch would add their
+    own ~1 us to each)."""
+    import torch
+
+    ngroups = max(1, calls // group)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(ngroups)]
+    torch.cuda.synchronize()
+    i = 0
+    for a, b in ev:
+        a.record(stream)
+        for _ in range(group):
+            step(i)
+            i += 1
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) / group for a, b in ev]
+    return statistics.median(ms), statistics.fmean(ms)
+
+
+def _graphed(step, dev, per_graph=10):
+    """``step`` captured ``per_graph`` times (i = 0 .. per_graph - 1) into one HIP graph; returns
+    a step function that replays it (one call = ``per_graph`` launches with no host gaps)."""
+    import torch
+
+    stream = torch.cuda.current_stream(dev)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(per_graph):
+                step(i, torch.cuda.current_stream(dev).cuda_stream)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    return graph
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: every core of this process's affinity mask, capped at the
+    host's CPU share per GPU when the environment states one (OMP_NUM_THREADS; the GPU boxes
+    set it to 16 and allot that many cores per GPU, whatever the affinity mask lists)."""
+    aff = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    cap = int(share) if share.isdigit() and int(share) > 0 else aff
+    return max(1, min(aff, cap)), aff
 
 
 def flops_per_fwd(b=B, h=H, n=N, d=D):
@@ -67,7 +138,7 @@ def cpu_baseline(gpu_o_sample, q_sample, k_sample, v_sample, heads_in_sample):
 
     from oracle import manual_attention_torch
 
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    cores, aff = cpu_threads()
     torch.set_num_threads(cores)
     q, k, v = q_sample.float().cpu(), k_sample.float().cpu(), v_sample.float().cpu()
     manual_attention_torch(q[:, :1], k[:, :1], v[:, :1])  # warm-up
@@ -87,11 +158,50 @@ def cpu_baseline(gpu_o_sample, q_sample, k_sample, v_sample, heads_in_sample):
         "kind": "port",
         "sample": (f"{heads_in_sample} of {B * H} (batch, head) pairs, N={N}, d={D}, of bench input "
                    f"set 0; torch {torch.__version__} fp32 manual path on {cores} threads of "
-                   f"{cpu_model()}, median of 3 runs = {sec:.3f} s; TFLOP/s on the same algorithmic "
-                   f"FLOP count as the GPU"),
+                   f"{cpu_model()} (affinity mask {aff} cores; threads = the host's CPU share per "
+                   f"GPU, OMP_NUM_THREADS), median of 3 runs = {sec:.3f} s; TFLOP/s on the same "
+                   f"algorithmic FLOP count as the GPU"),
         "seconds_per_sample": sec,
         "max_abs_diff_vs_gpu": max_err,
     }
+
+
+def cpu_baseline_configs():
+    """The same CPU path on BASELINE.json configs 1-4 at full shape, on the oracle's seeded
+    inputs (oracle.make_inputs); config 4's (B,H,N,N) fp32 scores (4.3 GB) are formed one
+    head at a time.  One warm-up, median of 3 runs each."""
+    import torch
+
+    from oracle import CONFIGS, make_inputs, manual_attention_torch
+
+    cores, _ = cpu_threads()
+    torch.set_num_threads(cores)
+    out = {}
+    for name in ("config1", "config2", "config3", "config4"):
+        cfg = CONFIGS[name]
+        q, k, v = (torch.from_numpy(x) for x in make_inputs(cfg))
+        chunked = cfg.N > 2048
+
+        def run():
+            if not chunked:
+                return manual_attention_torch(q, k, v)
+            for b in range(cfg.B):
+                for h in range(cfg.H):
+                    manual_attention_torch(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1])
+            return None
+
+        manual_attention_torch(q[:1, :1], k[:1, :1], v[:1, :1])
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        sec = statistics.median(times)
+        out[name] = {"seconds": round(sec, 4), "TFLOP/s": round(cfg.flops / sec / 1e12, 4),
+                     "shape": f"B{cfg.B} H{cfg.H} N{cfg.N} d{cfg.D}",
+                     "chunked": "one (b, h) head at a time" if chunked else "whole config"}
+    out["threads"] = cores
+    return out
 
 
 def cpu_model():
@@ -164,7 +274,7 @@ def time_generate(dev, runs=5, warmup=2):
     return out
 
 
-def time_strided_views(dev, steps, warmup):
+def time_strided_views(dev, steps=MIN_PER_CALL):
     """Same workload through tfgfa_fwd_bf16_strided with the operands of a GPT-2 block as they
     come out of the Q/K/V projections: (B, N, H, 64) buffers read as (B, H, N, 64) views and O
     written into a (B, N, H, 64) buffer (no copies before or after the kernel)."""
@@ -188,20 +298,12 @@ def time_strided_views(dev, steps, warmup):
         _C.fwd_strided(q.data_ptr(), q.stride(), k.data_ptr(), k.stride(), v.data_ptr(), v.stride(),
                        o.data_ptr(), o.stride(), lse.data_ptr(), B, H, N, D, SCALE, True, sh)
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(steps):
-        step(i)
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    _warm(step)
+    med, mean = _per_call_ms(step, stream, max(steps, MIN_PER_CALL))
     return {"layout": "q, k, v: (B, N, H, 64) buffers viewed (B, H, N, 64); o: (B, N, H, 64) buffer",
-            "ms_per_step": round(ms, 5), "value": round(flops_per_fwd() / (ms * 1e-3) / 1e12, 2),
-            "unit": "TFLOP/s", "steps": steps}
+            "ms_per_call_median": round(med, 5), "ms_per_call_mean": round(mean, 5),
+            "value": round(flops_per_fwd() / (med * 1e-3) / 1e12, 2),
+            "unit": "TFLOP/s", "calls": max(steps, MIN_PER_CALL)}
 
 
 DEC_SETS = 6  # 6 x 52 MB of K/V cache: more than the 256 MB Infinity Cache
@@ -214,7 +316,7 @@ def decode_bytes(b=B, h=H, n=N, d=D):
     return b * h * (2 * (n - 1) * d * 2 + 3 * d * 2 + 2 * d * 2 + d * 2 + 4)
 
 
-def time_decode(dev, steps, warmup):
+def time_decode(dev, steps=2000):
     """One decode step of attention at the GPT-2-XL shape: B=8, H=25, a 1024-row KV cache per
     head with 1023 valid rows, the new token appended (row 1023) and attended, O and LSE written.
     The step is HBM-bound: the figure of merit is GB/s against the 8 TB/s HBM peak."""
@@ -245,9 +347,7 @@ def time_decode(dev, steps, warmup):
                   o.data_ptr(), o.stride(), lse.data_ptr(), B, H, N, D, SCALE, ws.data_ptr(),
                   ws_bytes, sh)
 
-    for i in range(warmup):
-        step(i)
-    torch.cuda.synchronize()
+    _warm(step)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
@@ -276,8 +376,7 @@ def time_decode(dev, steps, warmup):
                           SCALE, ws.data_ptr(), ws_bytes, sh_cap)
     stream.wait_stream(side)
     replays = max(1, steps // per_graph)
-    for _ in range(max(1, warmup // per_graph)):
-        graph.replay()
+    _warm(lambda i: graph.replay(), min_calls=2)
     torch.cuda.synchronize()
     start.record(stream)
     for _ in range(replays):
@@ -345,9 +444,7 @@ def time_decode_split(dev, reps=20):
                 for i in range(per_graph):
                     step(i, torch.cuda.current_stream(dev).cuda_stream)
         stream.wait_stream(side)
-        for _ in range(3):
-            graph.replay()
-        torch.cuda.synchronize()
+        _warm(lambda i: graph.replay(), min_calls=3)
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record(stream)
@@ -369,6 +466,70 @@ def time_decode_split(dev, reps=20):
     return out
 
 
+CONFIG_SETS = {"config1": 4, "config2": 6, "config3": 4, "config4": 5}
+
+
+def time_configs(dev):
+    """Every BASELINE.json attention config (1-4) through the C ABI on this build's kernel, O + LSE
+    (the headline's outputs), plus config 3 through the drop-in O-only call: seeded inputs of
+    each config's distribution, input sets rotated so that the working set of one launch is
+    not left in the Infinity Cache by the previous one (config 1, 1.6 MB per set, stays
+    cache-resident), a warm-up of at least 0.1 s, then the median of 200 per-launch event
+    timings."""
+    import torch
+
+    from custom_flash_attn import _C
+    from oracle import CONFIGS
+
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    out = {}
+    legs = [("config1", True), ("config2", True), ("config3", True), ("config3_o_only", False),
+            ("config4", True)]
+    for leg, with_lse in legs:
+        cfg = CONFIGS[leg.split("_")[0]]
+        gen = torch.Generator(device=dev).manual_seed(cfg.seed)
+        sets = []
+        for _ in range(CONFIG_SETS[cfg.name]):
+            q, k, v = ((torch.randn(cfg.B, cfg.H, cfg.N, cfg.D, device=dev, generator=gen) * sg)
+                       .to(torch.bfloat16) for sg in (cfg.sigma_qk, cfg.sigma_qk, cfg.sigma_v))
+            o = torch.empty_like(q)
+            lse = torch.empty(cfg.B, cfg.H, cfg.N, device=dev, dtype=torch.float32)
+            sets.append((q, k, v, o, lse))
+
+        def step(i, s=sh, sets=sets, cfg=cfg, with_lse=with_lse):
+            q, k, v, o, lse = sets[i % len(sets)]
+            _C.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                   lse.data_ptr() if with_lse else 0, cfg.B, cfg.H, cfg.N, cfg.D, cfg.scale, True, s)
+
+        how = "direct launches from Python"
+        timed_step, group = step, 10
+        if cfg.name == "config1":
+            # A ~3 us kernel: launches from Python would leave the GPU idle between them, so
+            # 10 launches are captured in a HIP graph and the graph is replayed.
+            graph = _graphed(step, dev)
+            timed_step, group = (lambda i: graph.replay()), 1
+            how = "HIP graph of 10 launches, replayed"
+        _warm(timed_step)
+        med, mean = _per_call_ms(timed_step, stream, MIN_PER_CALL // (10 if group == 1 else 1), group)
+        if group == 1:
+            med, mean = med / 10, mean / 10
+        tf = cfg.flops / (med * 1e-3) / 1e12
+        hbm_ceiling = min(1.0, cfg.flops / cfg.bytes * PEAK_HBM_GBS * 1e9 / (PEAK_BF16_TFLOPS * 1e12))
+        out[leg] = {
+            "shape": f"B{cfg.B} H{cfg.H} N{cfg.N} d{cfg.D}", "outputs": "O + LSE" if with_lse else "O",
+            "ms_per_call_median": round(med, 5), "ms_per_call_mean": round(mean, 5),
+            "calls": MIN_PER_CALL, "timing": how, "input_sets_rotated": len(sets),
+            "value": round(tf, 2), "unit": "TFLOP/s",
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                         "hbm_ceiling_frac_of_mfma_peak": round(hbm_ceiling, 4)},
+        }
+        del sets
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -384,6 +545,8 @@ def main():
                     help="skip the token-generation leg (the reference's generate() benchmark)")
     ap.add_argument("--no-strided", action="store_true",
                     help="skip the second timing of the same workload on strided (B, N, H, 64) views")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config legs (BASELINE.json configs 1-4, per-launch medians)")
     ap.add_argument("--cpu-heads", type=int, default=200,
                     help="heads of the workload timed by the CPU baseline")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -438,6 +601,7 @@ def main():
                B, H, N, D, SCALE, True, sh)
 
     def timed(steps, warmup, with_lse):
+        _warm(lambda i: step(i, with_lse))  # clocks settle: >= 0.1 s of launches, untimed
         for i in range(warmup):
             step(i, with_lse)
         torch.cuda.synchronize()
@@ -486,15 +650,23 @@ def main():
         },
         "device": info,
     }
+    # Per-call view of the same leg: the median over 20 groups of 10 back-to-back launches.
+    med, mean = _per_call_ms(lambda i: step(i, True), stream)
+    result["ms_per_call_median"] = round(med, 5)
+    result["value_at_median"] = round(flops_per_fwd() / (med * 1e-3) / 1e12, 2)
     # The drop-in forward(q, k, v) returns O only: no LSE output, so the kernel instance without
-    # the fp32 probability sum that only the LSE needs.
-    ms_o = timed(max(1, args.steps // 2), max(1, args.warmup // 2), False)
-    result["o_only"] = {"outputs": "O (custom_flash_attn.forward)", "ms_per_step": round(ms_o, 5),
-                        "value": round(flops_per_fwd() / (ms_o * 1e-3) / 1e12, 2), "unit": "TFLOP/s"}
+    # the fp32 probability sum that only the LSE needs.  Its own warm-up and 200 launches.
+    _warm(lambda i: step(i, False))
+    med_o, mean_o = _per_call_ms(lambda i: step(i, False), stream)
+    result["o_only"] = {"outputs": "O (custom_flash_attn.forward)", "ms_per_call_median": round(med_o, 5),
+                        "ms_per_call_mean": round(mean_o, 5), "calls": MIN_PER_CALL,
+                        "value": round(flops_per_fwd() / (med_o * 1e-3) / 1e12, 2), "unit": "TFLOP/s"}
+    if not args.no_configs:
+        result["configs"] = time_configs(dev)
     if not args.no_strided:
-        result["strided_gpt2_views"] = time_strided_views(dev, max(1, args.steps // 2), max(1, args.warmup // 2))
+        result["strided_gpt2_views"] = time_strided_views(dev)
     if not args.no_decode:
-        result["decode"] = time_decode(dev, args.steps, args.warmup)
+        result["decode"] = time_decode(dev)
         result["decode_split"] = time_decode_split(dev)
     if not args.no_generate:
         result["generate"] = time_generate(dev)
@@ -503,6 +675,7 @@ def main():
         q, k, v, o = (t.reshape(1, B * H, N, D)[:, :nh] for t in sets[0][:4])
         torch.cuda.synchronize()
         result["cpu_baseline"] = cpu_baseline(o, q, k, v, nh)
+        result["cpu_baseline"]["by_config"] = cpu_baseline_configs()
     print(json.dumps(result), flush=True)
 
 

@@ -29,6 +29,17 @@
  *    call, so argument errors are reported identically with or without a GPU),
  *    < 0 the negated hipError_t of a failed HIP call.
  *  - Calls are reentrant; launches are asynchronous on the given stream.
+ *
+ * Numeric range of the forward (tfgfa_fwd, tfgfa_fwd_bf16, tfgfa_fwd_bf16_strided).
+ * Scores and sums are fp32.  The softmax offset of a row moves lazily: only when a
+ * probability taken against the current offset could exceed 2^64 (bf16) or 2^15 (fp16)
+ * does it jump to the row's running maximum (the reference moves it on every tile,
+ * src/cpp/headers/v1_implementation.hpp:121-128).  So every probability stays <= 2^64
+ * (bf16) / 2^15 (fp16), and the fp32 accumulators of P.V and of the sums stay finite while
+ *     N_k * max|V| < 2^64   (bf16; the reference's exact offset allows 2^128),
+ *     N_k * max|V| < 2^113  (fp16; always true, fp16 values are below 2^16).
+ * Past that bound a bf16 row may come out inf or NaN where the exact-offset reference
+ * stays finite.  LSE is not affected.
  */
 #ifndef TFGFA_H
 #define TFGFA_H
@@ -87,7 +98,7 @@ int tfgfa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* 
  * _flash_attn_forward(q, k, v, softmax_scale) (src/py/triton_implementation.py:184-197,
  * kernel :15-181): q (B, H, N_q, D), k and v (B, H, N_k, D), o like q, all strided
  * (4 element strides each, b/h/n/d, NULL = contiguous; rules as for
- * tfgfa_fwd_bf16_strided below with "n >= D" for "n >= 64"), dtype
+ * tfgfa_fwd_bf16_strided below), dtype
  * TFGFA_DTYPE_BF16 or TFGFA_DTYPE_F16, D any multiple of 8 from 8 to 128
  * (the Triton wrapper's d <= 128, :190), an explicit scale.  With causal == 1
  * the mask is top-left aligned as in the Triton kernel (:127): query i sees keys
@@ -111,7 +122,7 @@ int tfgfa_fwd(const void* q, const int64_t* q_strides,
  * (the reference's caller views and transposes, src/py/model_inference.py:64-66,
  * copies Q, K, V with .contiguous(), :86-90, and O again, :92).
  * Rules (TFGFA_ERR_STRIDE otherwise): dim stride 1; batch, head and row strides
- * non-negative multiples of 8; row stride >= 64; no two elements of O at one
+ * non-negative multiples of 8; row stride >= D; no two elements of O at one
  * address (checked: sorted by stride, each stride of a dimension of size > 1
  * exceeds the span of the smaller ones).  The stride of a dimension of size 1
  * is ignored.  (N + 128) * row stride * 2 must be < 2^31 (TFGFA_ERR_TOO_LARGE).

@@ -489,5 +489,40 @@ def test_gpt2_manual_and_functional_agree_on_cpu():
 def test_gpt2_rejects_unknown_impl():
     import model_inference as mi
 
-    with pytest.raises(ValueError, match="triton"):
-        mi.MultiHeadAttention(8, 8, 4, 0.0, 2, "triton")
+    with pytest.raises(ValueError, match="xla"):
+        mi.MultiHeadAttention(8, 8, 4, 0.0, 2, "xla")
+
+
+def test_gpt2_accepts_the_reference_impl_types():
+    """The reference's four-way dispatch (src/py/model_inference.py:68-90) constructs with every
+    impl_type it names; "hip" is this build's copy-free variant of "cuda"."""
+    import model_inference as mi
+
+    for impl in ("manual", "functional", "triton", "cuda", "hip"):
+        att = mi.MultiHeadAttention(8, 8, 4, 0.0, 2, impl)
+        assert att.impl_type == impl
+
+
+def test_decode_workspace_not_cached_under_graph_capture(monkeypatch):
+    """A decode() call made during graph capture gets its own workspace; eager calls share the
+    cached per-(device, stream) buffer.  Runs on CPU tensors with the capture state forced."""
+    import custom_flash_attn as cfa
+
+    dev = torch.device("cpu")
+    monkeypatch.setattr(cfa, "_WORKSPACES", {})
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    a = cfa._decode_workspace(dev, 256)
+    b = cfa._decode_workspace(dev, 256)
+    assert a.numel() >= 256 and b.numel() >= 256
+    assert a.data_ptr() != b.data_ptr() or a is not b
+    assert cfa._WORKSPACES == {}
+
+    class _S:
+        cuda_stream = 1234
+
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda d=None: _S())
+    c = cfa._decode_workspace(dev, 256)
+    d = cfa._decode_workspace(dev, 128)
+    assert c is d and c.numel() >= 256
+    assert list(cfa._WORKSPACES) == [(dev, 1234)]

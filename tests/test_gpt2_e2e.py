@@ -14,7 +14,9 @@ kernel's output).  The kernel run must stay within 1.5x the control's relative L
 (plus 1e-4), its relative L2 error must be below 2e-2, and the argmax agreement with the
 CPU logits must be at least 0.97x the control's.  The "hip" (strided, copy-free) and
 "cuda" (contiguous copies, as the reference calls the kernel) branches run the same kernel on
-the same values, so their logits must be bit-identical.
+the same values, so their logits must be bit-identical; so must the "triton" branch (the
+reference's route to its Triton wrapper, model_inference.py:82-83, served here by
+custom_flash_attn.flash_attn_forward on the same kernel).
 """
 import math
 import sys
@@ -72,7 +74,7 @@ def test_gpt2_medium_logits_match_cpu(gpt2_medium_cpu_reference):
         gpu = model.to("cuda:0")
         idx_d = idx.to("cuda:0")
         results, logits = {}, {}
-        for impl in ("hip", "cuda", "fp32_control"):
+        for impl in ("hip", "cuda", "triton", "fp32_control"):
             for blk in gpu.trf_blocks:
                 blk.att.impl_type = impl
             _say(f"config5: GPU forward impl={impl}")
@@ -87,13 +89,15 @@ def test_gpt2_medium_logits_match_cpu(gpt2_medium_cpu_reference):
         del mi.ATTENTION_IMPLS["fp32_control"]
         model.to("cpu")
     assert torch.equal(logits["hip"], logits["cuda"]), "strided and contiguous branches differ"
+    assert torch.equal(logits["hip"], logits["triton"]), "the triton branch differs from hip"
     hip, ctl = results["hip"], results["fp32_control"]
     assert hip[0] <= 1.5 * ctl[0] + 1e-4
     assert hip[0] < 2e-2
     assert hip[2] >= 0.97 * ctl[2]
 
 
-@pytest.mark.parametrize("impl,entry", [("hip", "attention"), ("cuda", "forward")])
+@pytest.mark.parametrize("impl,entry", [("hip", "attention"), ("cuda", "forward"),
+                                        ("triton", "flash_attn_forward")])
 def test_hip_attention_is_the_kernel(monkeypatch, impl, entry):
     """Both kernel branches must reach the native entry points (no silent fallback); the
     "hip" branch hands the kernel non-contiguous views and gets no copy back."""
@@ -116,3 +120,24 @@ def test_hip_attention_is_the_kernel(monkeypatch, impl, entry):
         out = model(torch.randint(0, 101, (2, 100), device="cuda:0"))
     assert out.shape == (2, 100, 101) and torch.isfinite(out).all()
     assert calls == [(torch.Size([2, 4, 100, 64]), impl == "cuda")] * 2
+
+
+def test_triton_impl_bitwise_equals_hip():
+    """impl_type="triton" (the reference's four-way dispatch, model_inference.py:68-90) runs
+    unchanged and gives logits bit-identical to "hip" on a small GPT."""
+    cfg = dict(mi.GPT_CONFIG_124M)
+    cfg.update({"emb_dim": 256, "n_layers": 2, "n_heads": 4, "vocab_size": 101,
+                "context_length": 160, "drop_rate": 0.0, "qkv_bias": True, "impl_type": "hip"})
+    model = mi.GPTModel(cfg).eval().to("cuda:0")
+    mi.init_gpt2_weights(model, 3)
+    idx = torch.randint(0, 101, (3, 150), device="cuda:0", generator=torch.Generator(device="cuda:0").manual_seed(4))
+    out = {}
+    for impl in ("hip", "triton"):
+        for blk in model.trf_blocks:
+            blk.att.impl_type = impl
+        with torch.no_grad():
+            out[impl] = model(idx)
+    torch.cuda.synchronize()
+    _say(f"triton vs hip: max|d|={(out['hip'] - out['triton']).abs().max().item():.3e}")
+    assert torch.isfinite(out["hip"]).all()
+    assert torch.equal(out["hip"], out["triton"])

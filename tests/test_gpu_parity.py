@@ -164,6 +164,18 @@ def test_config_full_tensor_vs_reference_cpu_path(name):
     assert worst <= TOL_MAX and total / count <= TOL_MEAN
 
 
+@pytest.mark.parametrize("name", ["config2", "config3", "config4"])
+def test_config_every_row_vs_fp64_oracle(name):
+    """O and LSE of every row of configs 2-4 against the fp64 C oracle (attention_ref.c, the
+    "manual" branch of src/py/model_inference.py:68-75 and the lse_i of
+    src/py/triton_implementation.py:153-154), no sampling."""
+    cfg, q, k, v = _config_inputs(name)
+    _say(f"{name} every row vs fp64 oracle (O and LSE)")
+    o, lse = _run(q, k, v, cfg.scale, True)
+    o_ref, lse_ref = attention_c(q, k, v, cfg.scale, True)
+    _check(o, lse, o_ref, lse_ref, f"{name} every row")
+
+
 # ------------------------------------------------------------------ reference test shapes
 
 

@@ -85,3 +85,68 @@ def test_extreme_score_patterns(kind, N, D, dtype):
     assert np.isfinite(o).all() and np.isfinite(lse).all(), "non-finite output"
     assert d.max() <= 2e-2 and d.mean() <= 2e-3
     assert (dl <= 1e-3 + 4e-7 * np.abs(l_ref)).all()
+
+
+def _range_case(N, v_scale, positive):
+    """Scores built so that the kernel's lazy offset never moves after a row's first 32 keys:
+    q = (16, 0, ...), k_j = (0, ...) for j < 32 and (20.75, 0, ...) after, so every later key
+    scores 16 * 20.75 / 8 = 41.5 (59.87 log2 units) above the offset set by keys 0..31 and each
+    probability is 2^59.87 (a lane's 16 of them sum to 2^63.87, under the 2^64 bound).  V is
+    v_scale times N(0, 1) clipped to +-7.99 (or |N(0, 1)| + 0.5 when ``positive``)."""
+    g = np.random.Generator(np.random.PCG64(N + int(math.log2(v_scale))))
+    q = np.zeros((1, 2, N, 64), dtype=np.float32)
+    k = np.zeros((1, 2, N, 64), dtype=np.float32)
+    q[..., 0] = 16.0
+    k[:, :, 32:, 0] = 20.75
+    z = g.standard_normal((1, 2, N, 64), dtype=np.float32)
+    z = np.abs(z) + 0.5 if positive else np.clip(z, -7.99, 7.99)
+    v = torch.from_numpy(z * np.float32(v_scale)).to(torch.bfloat16).float().numpy()
+    return q, k, v
+
+
+def test_bf16_range_inside_bound_matches_oracle():
+    """Just inside the documented bound of the lazy offset (include/tfgfa.h: bf16 O stays finite
+    while N_k * max|V| < 2^64): N = 1024, max|V| < 2^54, probabilities of 2^59.87 against an
+    offset that never moves.  O must be finite and match the fp64 oracle relative to V's
+    scale (the absolute 2e-2 / 2e-3 gates divided by 2^51); LSE as everywhere."""
+    N, vs = 1024, 2.0 ** 51
+    q, k, v = _range_case(N, vs, positive=False)
+    assert N * np.abs(v).max() < 2.0 ** 64
+    qd, kd, vd = (torch.from_numpy(x).to(torch.bfloat16).to(DEV) for x in (q, k, v))
+    o, lse = custom_flash_attn.forward_lse(qd, kd, vd)
+    o_only = custom_flash_attn.forward(qd, kd, vd)
+    torch.cuda.synchronize()
+    assert torch.equal(o_only.view(torch.int16), o.view(torch.int16)), "O-only call differs"
+    o_ref, l_ref = attention_np(q, k, v, 0.125, True)
+    o = o.float().cpu().numpy().astype(np.float64)
+    lse = lse.cpu().numpy().astype(np.float64)
+    d = np.abs(o - o_ref) / vs
+    dl = np.abs(lse - l_ref)
+    _say(f"range inside bound: N*max|V| = 2^{math.log2(N * np.abs(v).max()):.2f}; "
+         f"max|dO|/2^51={d.max():.3e} mean={d.mean():.3e} max|dLSE|={dl.max():.3e}")
+    assert np.isfinite(o).all() and np.isfinite(lse).all()
+    assert d.max() <= 2e-2 and d.mean() <= 2e-3
+    assert dl.max() <= 1e-3
+
+
+def test_bf16_range_past_bound_overflows_as_documented():
+    """Past the bound (all V near 2^62, N = 1024) the accumulated P.V of rows with enough keys
+    at 2^59.87 leaves fp32 and those rows come out non-finite, as include/tfgfa.h states (the
+    exact-offset reference stays finite there).  Rows whose sum stays below 2^128 and every LSE
+    are unaffected."""
+    N, vs = 1024, 2.0 ** 62
+    q, k, v = _range_case(N, vs, positive=True)
+    qd, kd, vd = (torch.from_numpy(x).to(torch.bfloat16).to(DEV) for x in (q, k, v))
+    o, lse = custom_flash_attn.forward_lse(qd, kd, vd)
+    torch.cuda.synchronize()
+    o_ref, l_ref = attention_np(q, k, v, 0.125, True)
+    o = o.float().cpu().numpy().astype(np.float64)
+    lse = lse.cpu().numpy().astype(np.float64)
+    assert np.isfinite(lse).all() and np.abs(lse - l_ref).max() <= 1e-3
+    # Rows 0..31 attend only to keys of probability 1: finite, equal to the oracle.
+    assert np.isfinite(o[:, :, :32]).all()
+    assert (np.abs(o[:, :, :32] - o_ref[:, :, :32]) / vs).max() <= 2e-2
+    # The last row's P.V sum is about 992 * 2^59.87 * 1.3 * 2^62 > 2^128.
+    finite_rows = np.isfinite(o).all(axis=-1)
+    _say(f"range past bound: non-finite rows {int((~finite_rows).sum())} of {finite_rows.size}")
+    assert not finite_rows[:, :, -1].any()

@@ -201,13 +201,22 @@ __device__ __forceinline__ i32x4 head_desc(const void* base, int N, int row_byte
 // track it: it would otherwise wait for every outstanding transfer before LDS reads it cannot
 // prove disjoint (it loses that proof at control-flow joins).  The only waits on these
 // transfers are the explicit vmcnt waits of the pipeline.
+// The transfer takes its LDS address from M0, a register the compiler reserves (a clobber of it
+// is not honoured).  So the statement saves M0 in a scalar register of its own, sets it, issues
+// the load and puts the saved value back: whatever the compiler keeps in M0 is unchanged after
+// the statement.  The s_nop is the one wait state GFX9 needs between an SALU write of M0 and an
+// LDS DMA that reads it.
 __device__ __forceinline__ void lds_transfer(i32x4 desc, uint32_t lds_base, int voff) {
+  uint32_t saved;
   asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds"
-      :
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
       : "s"(lds_base), "v"(voff), "s"(desc)
-      : "memory", "m0");
+      : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {

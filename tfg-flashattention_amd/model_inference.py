@@ -16,8 +16,11 @@ are not here.
   * ``"hip"`` - the same gfx950 kernel through custom_flash_attn.attention, which reads the
     (B, H, N, d) views of the projections in place and writes O straight into a (B, N, H, d)
     buffer: no copies on either side of the kernel.
-  There is no fallback for either: if the extension is missing they raise.
-  * ``"triton"`` is not provided (the Triton variant is not rebuilt).
+  * ``"triton"`` - the reference routes this to its Triton wrapper ``_flash_attn_forward``
+    (:82-83); here it is custom_flash_attn.flash_attn_forward, the drop-in for that wrapper
+    (same call, same asserts), running the same gfx950 kernel.  The Triton kernel itself is
+    not rebuilt.
+  There is no fallback for any of the three: if the extension is missing they raise.
 
 Behaviour difference, on purpose: the reference's "cuda" branch reshapes the kernel's
 (B, H, N, d) output straight to (B, N, H*d) without transposing (model_inference.py:92),
@@ -73,9 +76,18 @@ def _attn_hip(q, k, v, mask_bool, dropout):
     return out
 
 
+def _attn_triton(q, k, v, mask_bool, dropout):
+    # model_inference.py:82-83 (_flash_attn_forward on the (B, H, N, d) views), plus the
+    # transpose back to (B, N, H, d) that the reference's branch leaves out (:92).
+    import custom_flash_attn  # raises if the native extension is not built
+
+    return custom_flash_attn.flash_attn_forward(q, k, v).transpose(1, 2)
+
+
 ATTENTION_IMPLS: Dict[str, Callable] = {
     "manual": _attn_manual,
     "functional": _attn_functional,
+    "triton": _attn_triton,
     "hip": _attn_hip,
     "cuda": _attn_cuda,
 }
