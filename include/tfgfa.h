@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TFGFA_ABI_VERSION 5
+#define TFGFA_ABI_VERSION 6
 
 /* Status codes (> 0: invalid argument). */
 #define TFGFA_OK                 0
@@ -65,6 +65,7 @@ extern "C" {
 #define TFGFA_ERR_STRIDE         8  /* strides outside what the entry point takes         */
 #define TFGFA_ERR_CACHE          9  /* k_new/v_new given without cache_seqlens            */
 #define TFGFA_ERR_DTYPE         10  /* dtype is not a TFGFA_DTYPE_* value                 */
+#define TFGFA_ERR_SCRATCH       11  /* tfgfa_decode_noalloc: partials exceed its scratch    */
 
 /* Element types of q, k, v, o (fp32 accumulation and softmax either way). */
 #define TFGFA_DTYPE_BF16 0
@@ -222,6 +223,29 @@ int tfgfa_decode(const void* q, const int64_t* q_strides,
  * D = 64.  No counterpart in the reference.
  */
 size_t tfgfa_decode_workspace_size(int B, int H, int N_max, int D);
+
+/*
+ * tfgfa_decode without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Operands, results and errors as tfgfa_decode; the split
+ * partials go to a static 256 KiB scratch array of the library instead (one per GPU, held
+ * until the process ends), and the call allocates nothing.  Results are bitwise those of
+ * tfgfa_decode with a workspace of tfgfa_decode_workspace_size bytes.  Limit: the split the
+ * library chooses must fit the scratch, B*H*S*(D+1)*4 bytes <= 256 KiB, which holds on a
+ * 256-CU MI355X for every shape (at most 133 KiB); otherwise TFGFA_ERR_SCRATCH before any
+ * launch.  Every call on one GPU shares that GPU's scratch (it keeps the last call's
+ * partials; nothing needs to start at zero): calls that overlap on one GPU, e.g. on two
+ * streams at once, race and must be ordered by the caller.
+ */
+int tfgfa_decode_noalloc(const void* q, const int64_t* q_strides,
+                         void* k_cache, const int64_t* k_strides,
+                         void* v_cache, const int64_t* v_strides,
+                         const void* k_new, const int64_t* k_new_strides,
+                         const void* v_new, const int64_t* v_new_strides,
+                         const int* cache_seqlens,
+                         void* o, const int64_t* o_strides, float* lse,
+                         int B, int H, int N_max, int D, int dtype, float softmax_scale,
+                         void* hip_stream);
 
 /*
  * Human-readable text for a status code returned by any tfgfa_* function.

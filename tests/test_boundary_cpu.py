@@ -60,7 +60,8 @@ def lib():
 def test_library_exports_every_declared_symbol(lib):
     names = _header_functions()
     assert names == ["tfgfa_abi_version", "tfgfa_decode", "tfgfa_decode_bf16",
-                     "tfgfa_decode_workspace_bytes", "tfgfa_decode_workspace_size",
+                     "tfgfa_decode_noalloc", "tfgfa_decode_workspace_bytes",
+                     "tfgfa_decode_workspace_size",
                      "tfgfa_device_info", "tfgfa_fwd", "tfgfa_fwd_bf16", "tfgfa_fwd_bf16_strided",
                      "tfgfa_strerror"]
     for n in names:
@@ -76,7 +77,7 @@ def test_strerror_covers_every_status(lib):
     codes = [_header_define(n) for n in (
         "TFGFA_OK", "TFGFA_ERR_NULL_POINTER", "TFGFA_ERR_BAD_SHAPE", "TFGFA_ERR_HEAD_DIM",
         "TFGFA_ERR_SCALE", "TFGFA_ERR_CAUSAL_FLAG", "TFGFA_ERR_TOO_LARGE", "TFGFA_ERR_ALIGNMENT",
-        "TFGFA_ERR_STRIDE", "TFGFA_ERR_CACHE", "TFGFA_ERR_DTYPE")]
+        "TFGFA_ERR_STRIDE", "TFGFA_ERR_CACHE", "TFGFA_ERR_DTYPE", "TFGFA_ERR_SCRATCH")]
     msgs = [lib.tfgfa_strerror(c).decode() for c in codes]
     assert len(set(msgs)) == len(msgs)
     assert lib.tfgfa_strerror(12345).decode() == "unknown tfgfa status"
@@ -283,6 +284,22 @@ def test_general_decode_agrees_with_bf16_entry_on_d64_validation(lib):
                dict(q=P, kc=P, vc=P, o=P, ws=P + 8, ws_bytes=4096)):
         args = _decode_args(**kw)
         assert lib.tfgfa_decode(*_general(args)) == lib.tfgfa_decode_bf16(*args), kw
+
+
+def test_c_abi_noalloc_decode_validation(lib):
+    """tfgfa_decode_noalloc takes tfgfa_decode's arguments less the workspace and reports every
+    argument error the same way, before any HIP call (no compute call here)."""
+    lib.tfgfa_decode_noalloc.restype = ctypes.c_int
+    lib.tfgfa_decode_noalloc.argtypes = [ctypes.c_void_p, ctypes.c_void_p] * 5 + [
+        ctypes.c_void_p] * 4 + [ctypes.c_int] * 5 + [ctypes.c_float, ctypes.c_void_p]
+    for kw in (dict(), dict(B=-1), dict(N=-5), dict(D=36), dict(D=136), dict(scale=0.0),
+               dict(kn=P), dict(kn=P, vn=P), dict(B=0), dict(qs=_s3(192, 64, 2)),
+               dict(ks=_st(3 * 100 * 64, 100 * 64, 32, 1)), dict(os_=_s3(64, 64, 1)),
+               dict(N=1 << 24), dict(q=P + 8, kc=P, vc=P, o=P), dict(q=P, kc=P, vc=P, o=P, seq=P + 2)):
+        for dtype in (0, 1, 7):
+            general = _general(_decode_args(**kw), dtype)
+            noalloc = general[:20] + general[22:]
+            assert lib.tfgfa_decode_noalloc(*noalloc) == lib.tfgfa_decode(*general), (kw, dtype)
 
 
 def test_decode_workspace_size(lib):

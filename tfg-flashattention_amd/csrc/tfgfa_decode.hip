@@ -52,6 +52,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "tfgfa.h"
 
@@ -665,6 +666,38 @@ static bool vecs_overlap(const Vecs& v, int B, int H, int D) {
   return false;
 }
 
+// Scratch of tfgfa_decode_noalloc: the split partials of one call, in a file-scope device array
+// (one copy per GPU, held until the process ends) instead of a caller's workspace.  256 KiB
+// holds every split the library chooses on a 256-CU device (at most 2 workgroups per CU,
+// B*H*S <= 512, times (D + 1) floats: 133 KiB at D = 64, 132 KiB at D = 128).  The kernels get
+// the array's device address, looked up once per device with hipGetSymbolAddress; the array's
+// name itself is only a host-side stand-in.
+constexpr size_t kScratchBytes = 256 * 1024;
+static __device__ __attribute__((aligned(256))) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::once_flag g_scratch_once[kMaxDevices];
+static void* g_scratch_ptr[kMaxDevices];
+static int g_scratch_status[kMaxDevices];
+
+// This device's scratch address (first call on a device: the symbol lookup, with that device
+// current).  0, or the negated hipError_t of the failed lookup.
+static int device_scratch(void** out) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return -(int)e;
+  if (dev < 0 || dev >= kMaxDevices) return TFGFA_ERR_TOO_LARGE;
+  std::call_once(g_scratch_once[dev], [dev]() {
+    void* p = nullptr;
+    const hipError_t se = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_status[dev] = se == hipSuccess ? 0 : -(int)se;
+    g_scratch_ptr[dev] = se == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_status[dev] != 0) return g_scratch_status[dev];
+  *out = g_scratch_ptr[dev];
+  return TFGFA_OK;
+}
+
 // Bytes of one partial set (every head, one split) for head dim D: o_s[D] and lse_s.
 static size_t split_bytes(long long bh, int D) { return (size_t)bh * (size_t)(D + 1) * sizeof(float); }
 
@@ -676,7 +709,7 @@ static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
                        const int64_t* v_new_strides, const int* cache_seqlens, void* o,
                        const int64_t* o_strides, float* lse, int B, int H, int N_max, int D,
                        float softmax_scale, void* workspace, size_t workspace_bytes,
-                       void* hip_stream) {
+                       void* hip_stream, bool use_scratch = false) {
   if (B < 0 || H < 0 || N_max < 0) return TFGFA_ERR_BAD_SHAPE;
   if (D < 8 || D > kMaxD || (D & 7)) return TFGFA_ERR_HEAD_DIM;
   if (!(softmax_scale > 0.f) || !isfinite(softmax_scale)) return TFGFA_ERR_SCALE;
@@ -712,10 +745,20 @@ static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
   const int st = tfgfa_device_info(&cu, nullptr, nullptr, 0);
   if (st != TFGFA_OK) return st;
   const size_t per_split = split_bytes(bh, D);
-  const int ws_splits =
-      workspace ? (int)std::min((size_t)INT32_MAX, workspace_bytes / per_split) : 0;
   int S, C;
-  choose_split((int)bh, N_max, D, cu, std::max(1, ws_splits), &S, &C);
+  if (use_scratch) {
+    // The split the library would choose with an unbounded workspace must fit the scratch:
+    // then the result is bitwise that of tfgfa_decode with a full workspace.
+    choose_split((int)bh, N_max, D, cu, kMaxSplits, &S, &C);
+    if (S > 1 && (size_t)S * per_split > kScratchBytes) return TFGFA_ERR_SCRATCH;
+    const int sst = device_scratch(&workspace);
+    if (sst != TFGFA_OK) return sst;
+    workspace_bytes = kScratchBytes;
+  } else {
+    const int ws_splits =
+        workspace ? (int)std::min((size_t)INT32_MAX, workspace_bytes / per_split) : 0;
+    choose_split((int)bh, N_max, D, cu, std::max(1, ws_splits), &S, &C);
+  }
   if (bh * S > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
 
   const hipStream_t stream = (hipStream_t)hip_stream;
@@ -810,5 +853,28 @@ extern "C" int tfgfa_decode(const void* q, const int64_t* q_strides, void* k_cac
                                                v_new_strides, cache_seqlens, o, o_strides, lse, B,
                                                H, N_max, D, softmax_scale, workspace,
                                                workspace_bytes, hip_stream);
+  return TFGFA_ERR_DTYPE;
+}
+
+extern "C" int tfgfa_decode_noalloc(const void* q, const int64_t* q_strides, void* k_cache,
+                                    const int64_t* k_strides, void* v_cache,
+                                    const int64_t* v_strides, const void* k_new,
+                                    const int64_t* k_new_strides, const void* v_new,
+                                    const int64_t* v_new_strides, const int* cache_seqlens,
+                                    void* o, const int64_t* o_strides, float* lse, int B, int H,
+                                    int N_max, int D, int dtype, float softmax_scale,
+                                    void* hip_stream) {
+  if (dtype == TFGFA_DTYPE_BF16)
+    return tfgfa_dec::decode_step<__bf16>(q, q_strides, k_cache, k_strides, v_cache,
+                                             v_strides, k_new, k_new_strides, v_new,
+                                             v_new_strides, cache_seqlens, o, o_strides, lse, B, H,
+                                             N_max, D, softmax_scale, nullptr, 0, hip_stream,
+                                             true);
+  if (dtype == TFGFA_DTYPE_F16)
+    return tfgfa_dec::decode_step<_Float16>(q, q_strides, k_cache, k_strides, v_cache,
+                                               v_strides, k_new, k_new_strides, v_new,
+                                               v_new_strides, cache_seqlens, o, o_strides, lse, B,
+                                               H, N_max, D, softmax_scale, nullptr, 0, hip_stream,
+                                               true);
   return TFGFA_ERR_DTYPE;
 }
