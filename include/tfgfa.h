@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TFGFA_ABI_VERSION 6
+#define TFGFA_ABI_VERSION 7
 
 /* Status codes (> 0: invalid argument). */
 #define TFGFA_OK                 0
@@ -169,12 +169,16 @@ int tfgfa_fwd_bf16_strided(const void* q, const int64_t* q_strides,
  * of a chunk may be loaded (within the N_max rows of the cache) before the
  * length is known.
  *
- * workspace: device memory for split-sequence partials (16-byte aligned), or
- * NULL.  The cache sequence is split over up to
- * tfgfa_decode_workspace_bytes(B, H, N_max) / (B*H*260) workgroups per head,
- * merged by a second kernel; with NULL (or too small for two splits) each head
- * is one workgroup, correct but slower for small B*H.  Calls sharing a
- * workspace must be ordered on one stream.
+ * workspace: device memory for split-sequence work (16-byte aligned), or NULL:
+ * one arrival word per head (B*H*128 bytes rounded up to 256), then the
+ * partials (B*H*260 bytes per split).  When B*H leaves most CUs idle, the cache
+ * sequence is split over up to (workspace_bytes - arrival bytes) / (B*H*260)
+ * workgroups per head, and the workgroup that finishes last merges the head's
+ * partials (one kernel per step); with NULL (or too small for two splits) each
+ * head is one workgroup, correct but slower for small B*H.  The workspace needs
+ * no initialisation (every call leaves its arrival words at zero and installs
+ * its own random tag over whatever they hold).  Calls sharing a workspace must
+ * be ordered on one stream.
  */
 int tfgfa_decode_bf16(const void* q, const int64_t* q_strides,
                       void* k_cache, const int64_t* k_strides,
@@ -198,9 +202,8 @@ size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max);
  * dtype TFGFA_DTYPE_BF16 or TFGFA_DTYPE_F16 for q, the caches, k_new, v_new and
  * o (fp32 softmax either way), D a multiple of 8 in [8, 128] (the cache row
  * stride n >= D).  Everything else - operands, lengths, append, NaN for
- * invalid lengths, workspace - as tfgfa_decode_bf16, with the workspace split
- * count bounded by tfgfa_decode_workspace_size(B, H, N_max, D) /
- * (B*H*(D+1)*4).  With dtype TFGFA_DTYPE_BF16 and D = 64 the results are
+ * invalid lengths, workspace - as tfgfa_decode_bf16, with partials of
+ * B*H*(D+1)*4 bytes per split after the arrival words.  With dtype TFGFA_DTYPE_BF16 and D = 64 the results are
  * bitwise those of tfgfa_decode_bf16.  Replaces, as tfgfa_decode_bf16 does,
  * the per-token full forward of generate() (src/py/model_inference.py:199-228),
  * for the fp16 / d <= 128 surface of the Triton wrapper
@@ -227,15 +230,16 @@ size_t tfgfa_decode_workspace_size(int B, int H, int N_max, int D);
 /*
  * tfgfa_decode without a workspace argument, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
- * counterpart in the reference.  Operands, results and errors as tfgfa_decode; the split
- * partials go to a static 256 KiB scratch array of the library instead (one per GPU, held
- * until the process ends), and the call allocates nothing.  Results are bitwise those of
- * tfgfa_decode with a workspace of tfgfa_decode_workspace_size bytes.  Limit: the split the
- * library chooses must fit the scratch, B*H*S*(D+1)*4 bytes <= 256 KiB, which holds on a
- * 256-CU MI355X for every shape (at most 133 KiB); otherwise TFGFA_ERR_SCRATCH before any
- * launch.  Every call on one GPU shares that GPU's scratch (it keeps the last call's
- * partials; nothing needs to start at zero): calls that overlap on one GPU, e.g. on two
- * streams at once, race and must be ordered by the caller.
+ * counterpart in the reference.  Operands, results and errors as tfgfa_decode; the arrival
+ * words and split partials go to a static 320 KiB scratch array of the library instead (one
+ * per GPU, held until the process ends), and the call allocates nothing.  Results are
+ * bitwise those of tfgfa_decode with a workspace of tfgfa_decode_workspace_size bytes.
+ * Limit: the split the library chooses must fit the scratch, arrival words plus
+ * B*H*S*(D+1)*4 bytes <= 320 KiB, which holds on a 256-CU MI355X for every shape (at most
+ * 280 KiB); otherwise TFGFA_ERR_SCRATCH before any launch.  Every call on one GPU shares that
+ * GPU's scratch (it keeps the last call's partials, and its arrival words end at zero):
+ * calls that overlap on one GPU, e.g. on two streams at once, race and must be ordered by
+ * the caller.
  */
 int tfgfa_decode_noalloc(const void* q, const int64_t* q_strides,
                          void* k_cache, const int64_t* k_strides,

@@ -302,10 +302,18 @@ def test_c_abi_noalloc_decode_validation(lib):
             assert lib.tfgfa_decode_noalloc(*noalloc) == lib.tfgfa_decode(*general), (kw, dtype)
 
 
+def _decode_ws_bytes(B, H, N, D):
+    """Decode workspace layout: one 64-bit arrival word per head, 128 bytes apart, rounded up to
+    256 bytes; then one partial (D + 1 floats) per head per 128 cache rows."""
+    return -(-B * H * 128 // 256) * 256 + B * H * (-(-N // 128)) * (D + 1) * 4
+
+
 def test_decode_workspace_size(lib):
     assert lib.tfgfa_decode_workspace_size(8, 25, 1024, 64) == lib.tfgfa_decode_workspace_bytes(8, 25, 1024)
-    assert lib.tfgfa_decode_workspace_size(1, 1, 1, 128) == 129 * 4
-    assert lib.tfgfa_decode_workspace_size(2, 3, 300, 40) == 6 * 3 * 41 * 4
+    assert lib.tfgfa_decode_workspace_size(1, 1, 1, 128) == 256 + 129 * 4
+    assert lib.tfgfa_decode_workspace_size(2, 3, 300, 40) == 768 + 6 * 3 * 41 * 4
+    for args in ((8, 25, 1024, 64), (1, 16, 8192, 128), (3, 5, 77, 8)):
+        assert lib.tfgfa_decode_workspace_size(*args) == _decode_ws_bytes(*args)
     for bad in ((0, 1, 1, 64), (1, 0, 1, 64), (1, 1, 0, 64), (1, 1, 1, 0), (1, 1, 1, 12),
                 (1, 1, 1, 136)):
         assert lib.tfgfa_decode_workspace_size(*bad) == 0
@@ -323,9 +331,10 @@ def test_pybind_general_decode_raises_runtime_error_with_message():
 
 
 def test_decode_workspace_bytes(lib):
-    assert lib.tfgfa_decode_workspace_bytes(8, 25, 1024) == 8 * 25 * 8 * 65 * 4  # one slot per 128 rows
-    assert lib.tfgfa_decode_workspace_bytes(1, 1, 1) == 65 * 4
-    assert lib.tfgfa_decode_workspace_bytes(1, 16, 8193) == 16 * 65 * 65 * 4
+    # arrival words, then one partial slot per 128 rows
+    assert lib.tfgfa_decode_workspace_bytes(8, 25, 1024) == 25600 + 8 * 25 * 8 * 65 * 4
+    assert lib.tfgfa_decode_workspace_bytes(1, 1, 1) == 256 + 65 * 4
+    assert lib.tfgfa_decode_workspace_bytes(1, 16, 8193) == 2048 + 16 * 65 * 65 * 4
     for bad in ((0, 1, 1), (1, 0, 1), (1, 1, 0), (-1, 2, 3)):
         assert lib.tfgfa_decode_workspace_bytes(*bad) == 0
     assert _C.decode_workspace_bytes(8, 25, 1024) == lib.tfgfa_decode_workspace_bytes(8, 25, 1024)

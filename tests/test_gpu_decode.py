@@ -128,7 +128,10 @@ def test_split_and_single_workgroup_paths_agree():
     torch.cuda.synchronize()
     _check(o1, l1, o_ref, l_ref, "single workgroup")
     _check(o2, l2, o_ref, l_ref, "split")
-    assert _C.decode_workspace_bytes(B, H, N_max) == B * H * ((N_max + 127) // 128) * 65 * 4
+    # arrival words (128 bytes per head, rounded up to 256), then a 65-float partial per head per
+    # 128 rows
+    assert _C.decode_workspace_bytes(B, H, N_max) == (
+        -(-B * H * 128 // 256) * 256 + B * H * ((N_max + 127) // 128) * 65 * 4)
 
 
 def test_strided_cache_and_views_are_bitwise_equal():
@@ -232,8 +235,8 @@ def test_decode_argument_errors():
 
 
 def test_split_workspace_needs_no_initialisation_and_is_reusable():
-    """Small B*H splits each head over several workgroups whose partials a second kernel
-    merges; the workspace holds only those partials, so it may start as garbage and serves
+    """Small B*H splits each head over several workgroups; the one that arrives last merges
+    the partials.  The workspace (arrival words, then partials) may start as garbage and serves
     call after call."""
     B, H, N_max = 1, 4, 8192
     q, kc, vc = _case(B, H, N_max, 501)
@@ -252,3 +255,30 @@ def test_split_workspace_needs_no_initialisation_and_is_reusable():
     o_ref, l_ref = decode_np(q, kc, vc, [8000], 0.125)
     _check(outs[0][0], outs[0][1], o_ref, l_ref, "split B=1 H=4 L=8000, garbage workspace")
     _check(single[0], single[1], o_ref, l_ref, "single workgroup B=1 H=4 L=8000")
+
+
+def test_split_arrival_words_end_at_zero_whatever_they_held():
+    """The workspace starts with one 64-bit arrival word per head, 128 bytes apart:
+    tag << 16 | count.  Each call installs its own random tag, counts the arrivals of the
+    head's splits and leaves the word at zero.  Words of all ones, or holding another call's
+    tag with a partial count (as a call cut short would leave them), are replaced: the result
+    equals the oracle and the words end at zero."""
+    B, H, N_max = 1, 6, 4096
+    q, kc, vc = _case(B, H, N_max, 503)
+    sl = torch.tensor([N_max - 5], dtype=torch.int32, device=DEV)
+    qd, kd, vd = _dev(q), _dev(kc), _dev(vc)
+    nbytes = _C.decode_workspace_bytes(B, H, N_max)
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=DEV)
+    words = ws[: B * H * 128].view(torch.int64)[::16]  # 128 bytes apart
+    o_ref, l_ref = decode_np(q, kc, vc, [N_max - 5], 0.125)
+    first = custom_flash_attn.decode(qd, kd, vd, sl, return_lse=True, workspace=ws)
+    torch.cuda.synchronize()
+    _check(first[0], first[1], o_ref, l_ref, "split B=1 H=6, all-ones workspace")
+    assert torch.equal(words, torch.zeros_like(words)), words
+    for held in ((12345 << 16) | 3, (1 << 47) | 5, 1):
+        words.fill_(held)
+        again = custom_flash_attn.decode(qd, kd, vd, sl, return_lse=True, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(again[0].view(torch.int16), first[0].view(torch.int16)), hex(held)
+        assert torch.equal(again[1], first[1]), hex(held)
+        assert torch.equal(words, torch.zeros_like(words)), (hex(held), words)

@@ -118,8 +118,9 @@ def test_decode_steps_replay_from_a_graph():
 
 
 def test_split_decode_steps_replay_from_a_graph():
-    """Small B*H over a long cache: each step is the split decode kernel plus the merge kernel.
-    Both replay from one graph as the cache grows; every replay equals the eager step."""
+    """Small B*H over a long cache: each step splits every head over several workgroups, the
+    last to arrive merging them (arrival words in the workspace, reset to zero by each step).
+    The step replays from one graph as the cache grows; every replay equals the eager step."""
     B, H, N_max, D = 1, 4, 4096, 64
     kc = torch.zeros(B, H, N_max, D, dtype=torch.bfloat16, device=DEV)
     vc = torch.zeros_like(kc)

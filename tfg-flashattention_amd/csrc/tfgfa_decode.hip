@@ -15,10 +15,11 @@
 // per instruction, fp32 accumulate), which keeps the VALU time per byte below the HBM time.
 //
 // Work decomposition (split over the cache sequence)
-//   grid = B * H * S workgroups of 8 waves; workgroup (bh, s) covers keys [s*C, s*C + C) of
-//   head bh.  S = 1 while B*H covers at least half the CUs; below that the host splits each
-//   head so that the workgroups fill one round of workgroup slots (choose_split).  Inside a
-//   workgroup, wave w takes 32-key blocks w, w+8, w+16, ... of the chunk.
+//   grid = B * H * S workgroups of kW waves; workgroup (bh, s) covers keys [s*C, s*C + C) of
+//   head bh.  S = 1 (8-wave workgroups, one per head) while B*H covers at least half the CUs;
+//   below that the host splits each head over 4-wave workgroups that fill one round of
+//   workgroup slots (choose_split).  Inside a workgroup, wave w takes 32-key blocks w, w+kW,
+//   w+2kW, ... of the chunk.
 //   Lane l of a wave handles keys (block + l/4) and (block + l/4 + 16) and, for each 32-dim
 //   piece p of the row, head dims 32p + 8c .. 32p + 8c + 7 (c = l%4): one buffer_load_dwordx4
 //   per piece per key row per lane, so a wave instruction reads 16 rows x 64 contiguous bytes.
@@ -27,12 +28,33 @@
 //   block is computed.
 //   Each quad of lanes (one key column of the wave) runs its own online softmax over its
 //   keys, so the only cross-lane step per block is the 2-step DPP sum of a dot product within
-//   the quad; the 128 streams of a workgroup (in LDS) and, when S > 1, the workgroups are
+//   the quad; the 16 kW streams of a workgroup (in LDS) and, when S > 1, the workgroups are
 //   merged once at the end with the log-sum-exp rule
 //   o = sum_i 2^(m_i - M) o_i / sum_i 2^(m_i - M) l_i.
-//   S > 1: each workgroup writes its normalised partial (o_s[D], log2-domain lse_s) to the
-//   caller's workspace and decode_merge_kernel combines the S partials of a head.
 //   S = 1: the workgroup writes O and LSE itself.
+//   S > 1, one kernel: each workgroup writes its normalised partial (o_s[D], log2-domain
+//   lse_s) to the workspace and counts its arrival on the head's arrival word; the workgroup
+//   that arrives last merges the head's S partials and writes O and LSE (arrival protocol
+//   below).  A second, merging kernel would cost a launch and a drain per step (measured
+//   1.6 us for an empty kernel between graph-replayed kernels).
+//
+// Arrival protocol (S > 1).  The workspace starts with one 64-bit word per head, 128 bytes
+// apart (heads do not share a cache line: atomics on one line serialise), holding
+// tag << 16 | count.  The host draws a random nonzero 48-bit tag per call.
+//   start: wave 0 reads the word (before its first cache loads); when the tag differs (an idle
+//     word, 0, or memory never used as a workspace), lane 0 swaps in (tag, 0) with one
+//     compare-and-swap whose result is not needed: it fails only when another workgroup of
+//     the call already installed the tag.  The latency hides behind the cache loads.
+//   end: the partial is written with agent-coherent stores and waited for (s_waitcnt vmcnt(0):
+//     the stores have reached the device coherence point), then the count is incremented with
+//     one relaxed agent-scope atomic; the workgroup that reads count S - 1 resets the word to
+//     0 and reads the partials with agent-coherent loads.  Stores that bypass the
+//     non-coherent per-XCD L2 plus the wait stand in for a release fence, whose L2 writeback
+//     costs ~35 ns per workgroup serialised (measured: 30.7 us against 10.9 us per step at
+//     1 x 16 heads x 8192 rows).
+//   Every completed call leaves the words at 0, so the workspace needs no initialisation:
+//   garbage breaks the count only if its upper 48 bits equal this call's random tag.  Graph
+//   replays reuse the captured tag, each starting from the 0 the previous replay left.
 //
 // Cache append: with k_new/v_new given, key L_b = cache_seqlens[b] is the new token: the
 // workgroup whose chunk holds it stores k_new/v_new into cache row L_b and folds the values
@@ -52,6 +74,8 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <mutex>
 
 #include "tfgfa.h"
@@ -60,18 +84,20 @@ namespace tfgfa_dec {
 
 constexpr int kD = 64;                         // head dim of tfgfa_decode_bf16
 constexpr int kMaxD = 128;                     // largest head dim of tfgfa_decode
-constexpr int kThreads = 512;
-constexpr int kWaves = 8;
+constexpr int kWavesWhole = 8;                 // waves per workgroup, one workgroup per head
+constexpr int kWavesSplit = 4;                 // waves per workgroup of a split head
 constexpr int kKeysPerLane = 2;                // keys per lane per block (rows 16 apart)
 static_assert(kKeysPerLane % 2 == 0, "P.V pairs keys");
 constexpr int kWaveKeys = 16 * kKeysPerLane;   // keys per wave per block
-constexpr int kBlockKeys = kWaves * kWaveKeys; // keys per workgroup per block (chunk granule)
+constexpr int kBlockKeys = kWavesWhole * kWaveKeys;       // chunk granule, one workgroup per head
+constexpr int kSplitBlockKeys = kWavesSplit * kWaveKeys;  // chunk granule of a split head
 constexpr int kGroups = 16;                    // key columns per wave (4 lanes each)
-constexpr int kMergeThreads = 256;             // decode_merge_kernel: one wave per head
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kWorkspaceRows = 128;            // cache rows per split counted by the workspace
-static_assert(kBlockKeys % kWorkspaceRows == 0, "splits must not outnumber workspace slots");
+static_assert(kSplitBlockKeys % kWorkspaceRows == 0, "splits must not outnumber workspace slots");
+constexpr int kArriveStride = 128;             // bytes between the arrival words of two heads
+constexpr int kTagShift = 16;                  // arrival word: tag << 16 | count (count < 2^16)
 // A buffer offset past any num_records this file builds (those stay below 2^31 - 2^24): the
 // load returns zero without a memory access.  Used for the prefetch after the last block and
 // for the pieces of a row past the head dim.
@@ -313,23 +339,115 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// pstride: floats per partial (D + 1: o_s[D], lse_s).
-template <class Sh>
-__global__ __launch_bounds__(kThreads) void decode_kernel(
+// Partials of a split head (S > 1) are exchanged between workgroups on different XCDs, whose
+// L2 caches are not coherent with each other: the partial stores are agent-scope relaxed
+// atomic stores (written through to the device coherence point) and the merging loads use
+// the same device-scope cache policy (sc1), the forms the compiler emits for agent-scope
+// relaxed atomics.
+typedef unsigned long long u64;
+constexpr int kPolicyCoherent = 16;  // buffer-load cache policy bit sc1
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(__amdgpu_buffer_rsrc_t r, int off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kPolicyCoherent));
+}
+
+// Merge of the S partials (o_s[D], log2-domain lse_s; D + 1 floats each) of head bh by the
+// kW waves of the workgroup that arrived last: wave w folds splits w, w + kW, ... in batches
+// of kMergeBatch, every load of a batch in one memory round trip (one batch while
+// S <= kW * kMergeBatch); lane = head dim (and head dim + 64 when kTwo).  The split weights
+// 2^(lse_s - M) are formed in lanes 0..kMergeBatch-1 and read back as scalars; wave 0 folds
+// the kW wave sums from LDS and writes O and LSE.
+constexpr int kMaxSplits = 1024;
+constexpr int kMergeBatch = 16;
+template <class T, bool kTwo, int kW>
+__device__ __forceinline__ void merge_splits(const float* part, int bh, int S, int D, int wave,
+                                             int lane, bool valid, T* orow, float* lse_out,
+                                             float* sh_m, float* sh_w, float (*sh_acc)[128]) {
+  const int pstride = D + 1;
+  // The head's S partials as one buffer: offsets past it (splits >= S) read as zero.
+  const __amdgpu_buffer_rsrc_t pr = rows_rsrc(part + (long long)bh * S * pstride, S * pstride * 4);
+  float M = -INFINITY, wt = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int s0 = wave; s0 < S; s0 += kW * kMergeBatch) {
+    float x0[kMergeBatch], x1[kMergeBatch];
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {
+      const int sj = s0 + j * kW;
+      x0[j] = load_coherent(pr, (sj * pstride + lane) * 4);
+      x1[j] = kTwo ? load_coherent(pr, (sj * pstride + 64 + lane) * 4) : 0.f;
+    }
+    const int sl = s0 + (lane & (kMergeBatch - 1)) * kW;  // the split whose lse this lane reads
+    const float v = load_coherent(pr, (sl * pstride + D) * 4);
+    const float lse_j = (lane < kMergeBatch && sl < S) ? v : -INFINITY;
+    const float Mn = fmaxf(M, wave_max(lse_j));
+    const float Mn_use = (Mn == -INFINITY) ? 0.f : Mn;
+    const float a = exp2f(M - Mn_use);  // 0 before the first batch with a key
+    wt *= a;
+    o0 *= a;
+    o1 *= a;
+    const float w = exp2f(lse_j - Mn_use);  // 0 for splits past S or without keys
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; ++j) {
+      const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+      wt += wj;
+      o0 = fmaf(wj, x0[j], o0);
+      if (kTwo) o1 = fmaf(wj, x1[j], o1);
+    }
+    M = Mn;
+  }
+  if (lane == 0) {
+    sh_m[wave] = M;
+    sh_w[wave] = wt;
+  }
+  sh_acc[wave][lane] = o0;
+  if (kTwo) sh_acc[wave][64 + lane] = o1;
+  __syncthreads();
+  if (wave != 0) return;
+  float Mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kW; ++i) Mx = fmaxf(Mx, sh_m[i]);
+  const float Mx_use = (Mx == -INFINITY) ? 0.f : Mx;
+  float W = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kW; ++i) {
+    const float f = exp2f(sh_m[i] - Mx_use);
+    W = fmaf(f, sh_w[i], W);
+    a0 = fmaf(f, sh_acc[i][lane], a0);
+    if (kTwo) a1 = fmaf(f, sh_acc[i][64 + lane], a1);
+  }
+  if (lane < D) store_o<T>(orow + lane, W > 0.f ? a0 / W : 0.f, valid);
+  if (kTwo && lane + 64 < D) store_o<T>(orow + 64 + lane, W > 0.f ? a1 / W : 0.f, valid);
+  if (lse_out != nullptr && lane == 0)
+    store_lse(lse_out, W > 0.f ? (Mx + log2f(W)) * kLn2 : -INFINITY, valid);
+}
+
+// kW waves per workgroup: kWavesWhole for one workgroup per head (S = 1: O and LSE written
+// directly), kWavesSplit for S > 1 splits per head (part holds the partials, D + 1 floats each;
+// arrive the heads' arrival words; tag this call's 48-bit tag).
+template <class Sh, int kW>
+__global__ __launch_bounds__(64 * kW) void decode_kernel(
     const typename Sh::T* __restrict__ Q, Vecs qs, typename Sh::T* Kc, Rows ks,
     typename Sh::T* Vc, Rows vs, const typename Sh::T* __restrict__ Kn, Vecs kns,
     const typename Sh::T* __restrict__ Vn, Vecs vns, const int* __restrict__ seqlens,
     typename Sh::T* __restrict__ O, Vecs os, float* __restrict__ LSE, float* __restrict__ part,
-    int H, int N_max, int D, int S, int C, float scale_log2) {
+    u64* __restrict__ arrive, u64 tag, int H, int N_max, int D, int S, int C, float scale_log2) {
   typedef typename Sh::T T;
   constexpr int kDP = Sh::kDP;
   constexpr int kDm = Sh::kDm;
-  constexpr int kStreams = kWaves * kGroups;       // softmax streams of the workgroup
+  constexpr bool kSplit = kW == kWavesSplit;  // then S > 1
+  static_assert(kW == kWavesSplit || kW == kWavesWhole, "two workgroup shapes");
+  constexpr int kThreads = 64 * kW;
+  constexpr int kBlockKeysW = kW * kWaveKeys;      // keys per workgroup per block
+  constexpr int kStreams = kW * kGroups;           // softmax streams of the workgroup
   constexpr int kParts = kThreads / kDm;           // first-level merge: streams in kParts parts
   constexpr int kPerPart = kStreams / kParts;
   __shared__ float sh_o[kStreams][kDm + 1];        // +1: stream-major writes, dim-major reads
-  __shared__ float sh_l[kStreams], sh_wm[kWaves];
+  __shared__ float sh_l[kStreams], sh_wm[kW];
   __shared__ float sh_po[kParts][kDm], sh_pm[kParts], sh_pl[kParts];
+  __shared__ float sh_mm[kSplit ? kW : 1], sh_mw[kSplit ? kW : 1];  // merge_splits
+  __shared__ float sh_macc[kSplit ? kW : 1][128];
+  __shared__ int sh_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -353,6 +471,15 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   const int v_lane = g * vrow + 16 * c;
   const int c0 = s * C;
   int kb = c0 + wave * kWaveKeys;  // this wave's first block
+  // S > 1: this head's arrival word, read by wave 0 ahead of its cache loads.
+  u64* const aw = kSplit ? reinterpret_cast<u64*>(reinterpret_cast<char*>(arrive) +
+                                                  (long long)bh * kArriveStride)
+                         : nullptr;
+  u64 aw_start = 0;
+  if (kSplit) {
+    if (wave == 0) aw_start = __hip_atomic_load(aw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   // The first block's loads go out before the cache length arrives from memory: over the whole
   // allocation (N_max rows, all addressable), with the rows at or past the length zeroed once
   // it is known (below), so no stale or appended-row value reaches the sums.
@@ -417,7 +544,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
   // not read from the cache; wave 0 folds it in after the loop.
   const int ce = min(c1, Lc);
   if (kb < ce) {  // then kb < min(c0 + C, N_max): A was loaded
-    const int nblk = (ce - kb + kBlockKeys - 1) / kBlockKeys;  // this wave's blocks
+    const int nblk = (ce - kb + kBlockKeysW - 1) / kBlockKeysW;  // this wave's blocks
 #pragma unroll
     for (int r = 0; r < kKeysPerLane; ++r)
       if (kb + g + 16 * r >= Lr)
@@ -436,22 +563,32 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     // left alone, the scheduler hoists the (independent) dot products of the next block, which
     // then wait for the loads just issued.
     for (int t = 0; t + 2 <= nblk; t += 2) {
-      load_block<Sh>(B, kd, vd, krow, vrow, kb + kBlockKeys, true, k_lane, v_lane, pmask);
+      load_block<Sh>(B, kd, vd, krow, vrow, kb + kBlockKeysW, true, k_lane, v_lane, pmask);
       __builtin_amdgcn_sched_barrier(0);
       block_update<Sh>(A, qp, scale_log2, kb + g, ce, m, l, o);
       __builtin_amdgcn_sched_barrier(0);
-      kb += kBlockKeys;
-      load_block<Sh>(A, kd, vd, krow, vrow, kb + kBlockKeys, t + 2 < nblk, k_lane, v_lane, pmask);
+      kb += kBlockKeysW;
+      load_block<Sh>(A, kd, vd, krow, vrow, kb + kBlockKeysW, t + 2 < nblk, k_lane, v_lane, pmask);
       __builtin_amdgcn_sched_barrier(0);
       block_update<Sh>(B, qp, scale_log2, kb + g, ce, m, l, o);
       __builtin_amdgcn_sched_barrier(0);
-      kb += kBlockKeys;
+      kb += kBlockKeysW;
     }
     if (nblk & 1) block_update<Sh>(A, qp, scale_log2, kb + g, ce, m, l, o);
   }
   if (has_new && wave == 0) new_key_update<Sh>(k_app, v_app, qp, scale_log2, g == 0, m, l, o);
+  // Install this call's tag (count 0) unless a workgroup of the call already has; a failed
+  // swap means exactly that, so its result is not needed.  Placed after the cache loop, where
+  // every load (the word's first) has arrived: waiting for the word earlier would hold back
+  // the loads issued after it.  It precedes this workgroup's count increment (same address,
+  // program order).
+  if (kSplit && wave == 0 && lane == 0 && (aw_start >> kTagShift) != tag) {
+    u64 expected = aw_start;
+    __hip_atomic_compare_exchange_strong(aw, &expected, tag << kTagShift, __ATOMIC_RELAXED,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
-  // Merge the workgroup's 128 streams (16 key columns x 8 waves) in two LDS rounds:
+  // Merge the workgroup's 16 kW streams (16 key columns x kW waves) in two LDS rounds:
   //  1. each wave scales its streams once by 2^(m - M_w), M_w its largest stream maximum (row
   //     rotations and lane reads, no LDS), and writes them to LDS; thread t sums the streams
   //     of part t/kDm (kWavesPerPart whole waves) for head dim t%kDm, rescaling the waves'
@@ -498,95 +635,49 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(
     }
   }
   __syncthreads();
-  if (tid >= kDm || (Sh::kMaskD && tid >= D)) return;
-  const int d = tid;
-  float M = -INFINITY;
+  const bool writer = tid < kDm && !(Sh::kMaskD && tid >= D);  // thread d: head dim d
+  if (!kSplit && !writer) return;
+  if (writer) {
+    const int d = tid;
+    float M = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < kParts; ++i) M = fmaxf(M, sh_pm[i]);
-  const float M_use = (M == -INFINITY) ? 0.f : M;
-  float lt = 0.f, ot = 0.f;
+    for (int i = 0; i < kParts; ++i) M = fmaxf(M, sh_pm[i]);
+    const float M_use = (M == -INFINITY) ? 0.f : M;
+    float lt = 0.f, ot = 0.f;
 #pragma unroll
-  for (int i = 0; i < kParts; ++i) {
-    const float w = exp2f(sh_pm[i] - M_use);
-    lt = fmaf(w, sh_pl[i], lt);
-    ot = fmaf(w, sh_po[i][d], ot);
-  }
-  const float on = lt > 0.f ? ot / lt : 0.f;
-  const float lse2 = lt > 0.f ? M + log2f(lt) : -INFINITY;
-  if (S == 1) {
-    store_o<T>(O + b * os.b + h * os.h + d, on, valid);
-    if (LSE != nullptr && d == 0) store_lse(LSE + bh, lse2 * kLn2, valid);
-  } else {
+    for (int i = 0; i < kParts; ++i) {
+      const float w = exp2f(sh_pm[i] - M_use);
+      lt = fmaf(w, sh_pl[i], lt);
+      ot = fmaf(w, sh_po[i][d], ot);
+    }
+    const float on = lt > 0.f ? ot / lt : 0.f;
+    const float lse2 = lt > 0.f ? M + log2f(lt) : -INFINITY;
+    if (!kSplit) {
+      store_o<T>(O + b * os.b + h * os.h + d, on, valid);
+      if (LSE != nullptr && d == 0) store_lse(LSE + bh, lse2 * kLn2, valid);
+      return;
+    }
     float* pp = part + ((long long)bh * S + s) * (D + 1);
-    pp[d] = on;
-    if (d == 0) pp[D] = lse2;
+    store_coherent(pp + d, on);
+    if (d == 0) store_coherent(pp + D, lse2);
   }
-}
-
-// Combines the S partials of each head: one wave per head, lane = head dim (and head dim + 64).
-// The loads of a batch of kMergeBatch splits - every lane's partial values of those splits and
-// the splits' log-sum-exps - go out together, one memory round trip per batch (one in all for
-// S <= kMergeBatch); the weights 2^(lse_s - M) are formed in lanes 0..kMergeBatch-1 and read
-// back as scalars.  (Loops with one dependent load per split, or four at a time, cost 0.5-1.7
-// us more per graph-replayed step at the split shapes measured.)
-constexpr int kMaxSplits = 1024;
-constexpr int kMergeBatch = 16;
-__device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t r, int off) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-}
-// kTwo: D > 64, every lane folds head dims lane and lane + 64.
-template <class T, bool kTwo>
-__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
-    const float* __restrict__ part, const int* __restrict__ seqlens, T* __restrict__ O, Vecs os,
-    float* __restrict__ LSE, int BH, int H, int N_max, int D, int S, bool append) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPR descriptors
-  const int bh = blockIdx.x * (kMergeThreads / 64) + wave;
-  if (bh >= BH) return;
-  const int lane = threadIdx.x & 63;
-  const int b = bh / H, h = bh - b * H;
-  const int Lc = seqlens ? seqlens[b] : N_max;
-  const int pstride = D + 1;
-  // The head's S partials as one buffer: offsets past it read as zero.
-  const __amdgpu_buffer_rsrc_t pr = rows_rsrc(part + (long long)bh * S * pstride, S * pstride * 4);
-  const int js = lane & (kMergeBatch - 1);  // the split whose log-sum-exp this lane reads
-  float x0[kMergeBatch], x1[kMergeBatch], lse_j = -INFINITY;
-  auto load_batch = [&](int s0) {
-#pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
-      x0[j] = load_f32(pr, ((s0 + j) * pstride + lane) * 4);
-      x1[j] = kTwo ? load_f32(pr, ((s0 + j) * pstride + 64 + lane) * 4) : 0.f;
-    }
-    const float v = load_f32(pr, ((s0 + js) * pstride + D) * 4);
-    lse_j = s0 + js < S ? v : -INFINITY;
-  };
-  float M;
-  if (S <= kMergeBatch) {
-    load_batch(0);
-    M = wave_max(lse_j);
-  } else {
-    float mx = -INFINITY;
-    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, load_f32(pr, (s * pstride + D) * 4));
-    M = wave_max(mx);
+  if (!kSplit) return;
+  // S > 1 (every thread of the workgroup is here): the partial is at the coherence point once
+  // the writing waves' stores are acknowledged; then count the arrival.  The workgroup that
+  // arrives last resets the word and merges the head.
+  if (tid < kDm) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const u64 old = __hip_atomic_fetch_add(aw, (u64)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = (old & ((1ull << kTagShift) - 1)) == (u64)(S - 1);
+    if (last) __hip_atomic_store(aw, (u64)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_last = last;
   }
-  const float M_use = (M == -INFINITY) ? 0.f : M;
-  float wt = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int s0 = 0; s0 < S; s0 += kMergeBatch) {
-    if (S > kMergeBatch) load_batch(s0);
-    const float w = exp2f(lse_j - M_use);  // 0 for splits past S
-#pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
-      const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
-      wt += wj;
-      o0 = fmaf(wj, x0[j], o0);
-      if (kTwo) o1 = fmaf(wj, x1[j], o1);
-    }
-  }
-  const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
-  T* orow = O + b * os.b + h * os.h;
-  if (lane < D) store_o<T>(orow + lane, wt > 0.f ? o0 / wt : 0.f, valid);
-  if (kTwo && lane + 64 < D) store_o<T>(orow + 64 + lane, wt > 0.f ? o1 / wt : 0.f, valid);
-  if (LSE != nullptr && lane == 0)
-    store_lse(LSE + bh, wt > 0.f ? (M + log2f(wt)) * kLn2 : -INFINITY, valid);
+  __syncthreads();
+  if (!sh_last) return;
+  asm volatile("" ::: "memory");  // the partial loads stay after the arrival count
+  merge_splits<T, (kDm > 64), kW>(part, bh, S, D, wave, lane, valid, O + b * os.b + h * os.h,
+                                  LSE != nullptr ? LSE + bh : nullptr, sh_mm, sh_mw, sh_macc);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -594,35 +685,36 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
 
 // Splits for a cache of N_max rows of head dim D.  One 8-wave workgroup per head keeps 128 KiB
 // of K/V loads in flight, enough to stream at HBM rate from one CU, so heads are not split
-// while B*H covers at least half the CUs (no partials, no merge kernel; measured: two splits
-// per head at B*H = 200 cost 30% more).  Below that, a head is split so that the workgroups
-// fill one round of the workgroup slots (two per CU for D <= 64, whose 120 VGPRs let two
-// 8-wave workgroups share a CU; one for D > 64), rounding down so that no slot runs two, and
-// no split holds less than kSplitBytes of K and V (one key block at least).  Measured with the
-// merge kernel below (graph-replayed steps, caches rotating through HBM): 1 x 16 heads x 8192
-// rows 18.6 us with 2048-row splits -> 13.7 us; D = 128, 1 x 16 x 8192: 32.9 -> 21.3 us;
-// 1 x 8 x 2048: 14.1 -> 8.9 us.  Chunks are a multiple of kBlockKeys, no split is empty.
-constexpr int kSplitBytes = 64 * 1024;
-// Caches of fewer key blocks are not split: the merge kernel costs more than it saves there
-// (1 x 25 heads x 512 rows: 6.1 us as one workgroup per head, 7.6 us split; x 1024 rows: 8.5
-// against 7.9 us).
-constexpr int kMinSplitBlocks = 4;
+// while B*H covers at least half the CUs (no partials, no arrival count; measured: two splits
+// per head at B*H = 200 cost 30% more).  Below that, a head is split over 4-wave workgroups,
+// two per CU, rounding down so that no slot runs two, and no split holds less than
+// kSplitBytes of K and V (one key block at least).  Measured (graph-replayed steps, caches
+// rotating through HBM; two-kernel split with 8-wave workgroups -> this one-kernel split):
+// 1 x 16 heads x 8192 rows 12.3 -> 10.3 us, 1 x 25 x 1024 7.9 -> 6.5 us.  Chunks are a
+// multiple of kSplitBlockKeys, no split is empty.
+constexpr int kSplitBytes = 32 * 1024;
+// Caches of fewer split blocks (1024 rows) are not split: at 1 x 25 heads x 512 rows one
+// workgroup per head takes 6.1 us, the split 6.5 us; at 1024 rows the split wins.
+constexpr int kMinSplitBlocks = 8;
+constexpr int kSplitSlotsPerCu = 2;
 static void choose_split(int BH, int N_max, int D, int cu_count, int max_splits, int* S_out,
                          int* C_out) {
-  const int blocks = std::max(1, (N_max + kBlockKeys - 1) / kBlockKeys);
-  int S = 1;
-  if (2 * BH < cu_count && blocks >= kMinSplitBlocks) {
-    const int slots = cu_count * (D <= 64 ? 2 : 1);
-    S = std::max(1, slots / BH);
-    const int split_keys = std::max(kBlockKeys, kSplitBytes / (4 * D));
+  const int sblocks = std::max(1, (N_max + kSplitBlockKeys - 1) / kSplitBlockKeys);
+  if (2 * BH < cu_count && sblocks >= kMinSplitBlocks) {
+    int S = std::max(1, kSplitSlotsPerCu * cu_count / BH);
+    const int split_keys = std::max(kSplitBlockKeys, kSplitBytes / (4 * D));
     S = std::min(S, (N_max + split_keys - 1) / split_keys);
+    S = std::max(1, std::min(std::min(S, max_splits), kMaxSplits));
+    const int C = (sblocks + S - 1) / S * kSplitBlockKeys;
+    S = (N_max + C - 1) / C;
+    if (S > 1) {
+      *S_out = S;
+      *C_out = C;
+      return;
+    }
   }
-  S = std::min(S, blocks);
-  S = std::max(1, std::min(std::min(S, max_splits), kMaxSplits));
-  const int C = (blocks + S - 1) / S * kBlockKeys;
-  S = std::max(1, (N_max + C - 1) / C);
-  *S_out = S;
-  *C_out = C;
+  *S_out = 1;  // one chunk of the whole cache
+  *C_out = std::max(1, (N_max + kBlockKeys - 1) / kBlockKeys) * kBlockKeys;
 }
 
 static bool rows_ok(const int64_t* st, int B, int H, int N_max, int D, Rows* out) {
@@ -666,13 +758,15 @@ static bool vecs_overlap(const Vecs& v, int B, int H, int D) {
   return false;
 }
 
-// Scratch of tfgfa_decode_noalloc: the split partials of one call, in a file-scope device array
-// (one copy per GPU, held until the process ends) instead of a caller's workspace.  256 KiB
-// holds every split the library chooses on a 256-CU device (at most 2 workgroups per CU,
-// B*H*S <= 512, times (D + 1) floats: 133 KiB at D = 64, 132 KiB at D = 128).  The kernels get
+// Scratch of tfgfa_decode_noalloc: the arrival words and split partials of one call, in a
+// file-scope device array (one copy per GPU, held until the process ends) instead of a
+// caller's workspace.  320 KiB holds every split the library chooses on a 256-CU device:
+// B*H < 128 split heads (16 KiB of arrival words) and at most 2 workgroups per CU,
+// B*H*S <= 512, times (D + 1) floats (133 KiB at D = 64, 264 KiB at D = 128).  The kernels get
 // the array's device address, looked up once per device with hipGetSymbolAddress; the array's
-// name itself is only a host-side stand-in.
-constexpr size_t kScratchBytes = 256 * 1024;
+// name itself is only a host-side stand-in.  Zero at load; every call leaves its arrival
+// words at zero.
+constexpr size_t kScratchBytes = 320 * 1024;
 static __device__ __attribute__((aligned(256))) float scratch[kScratchBytes / sizeof(float)];
 
 constexpr int kMaxDevices = 64;
@@ -700,6 +794,27 @@ static int device_scratch(void** out) {
 
 // Bytes of one partial set (every head, one split) for head dim D: o_s[D] and lse_s.
 static size_t split_bytes(long long bh, int D) { return (size_t)bh * (size_t)(D + 1) * sizeof(float); }
+// Bytes of the arrival words at the start of a workspace: one per head, kArriveStride apart.
+static size_t arrive_bytes(long long bh) { return ((size_t)bh * kArriveStride + 255) / 256 * 256; }
+
+// A random nonzero 48-bit tag per call (splitmix64 over a process-wide counter and a seed from
+// the clock and an address), so that no word left in memory by anything else is likely to
+// carry it.
+static u64 splitmix64(u64 x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+static u64 next_tag() {
+  static std::atomic<u64> counter{0};
+  static const u64 seed =
+      splitmix64((u64)std::chrono::steady_clock::now().time_since_epoch().count() ^
+                 (u64)(uintptr_t)&counter);
+  const u64 t = splitmix64(seed + counter.fetch_add(1, std::memory_order_relaxed)) &
+                ((1ull << (64 - kTagShift)) - 1);
+  return t ? t : 1;
+}
 
 // The decode step for one element type: argument checks, split choice, launches.
 template <class T>
@@ -745,18 +860,20 @@ static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
   const int st = tfgfa_device_info(&cu, nullptr, nullptr, 0);
   if (st != TFGFA_OK) return st;
   const size_t per_split = split_bytes(bh, D);
+  const size_t ab = arrive_bytes(bh);
   int S, C;
   if (use_scratch) {
     // The split the library would choose with an unbounded workspace must fit the scratch:
     // then the result is bitwise that of tfgfa_decode with a full workspace.
     choose_split((int)bh, N_max, D, cu, kMaxSplits, &S, &C);
-    if (S > 1 && (size_t)S * per_split > kScratchBytes) return TFGFA_ERR_SCRATCH;
+    if (S > 1 && ab + (size_t)S * per_split > kScratchBytes) return TFGFA_ERR_SCRATCH;
     const int sst = device_scratch(&workspace);
     if (sst != TFGFA_OK) return sst;
     workspace_bytes = kScratchBytes;
   } else {
-    const int ws_splits =
-        workspace ? (int)std::min((size_t)INT32_MAX, workspace_bytes / per_split) : 0;
+    const int ws_splits = workspace && workspace_bytes > ab
+                              ? (int)std::min((size_t)INT32_MAX, (workspace_bytes - ab) / per_split)
+                              : 0;
     choose_split((int)bh, N_max, D, cu, std::max(1, ws_splits), &S, &C);
   }
   if (bh * S > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
@@ -769,12 +886,22 @@ static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
   const T* knt = static_cast<const T*>(k_new);
   const T* vnt = static_cast<const T*>(v_new);
   T* ot = static_cast<T*>(o);
-  float* ws = static_cast<float*>(workspace);
-  const dim3 grid((unsigned)(bh * S)), block(kThreads);
-#define TFGFA_DECODE_LAUNCH(kDP, kMask)                                                        \
-  hipLaunchKernelGGL((decode_kernel<DShape<T, kDP, kMask>>), grid, block, 0, stream, qt, qs, kc, \
-                     ks, vc, vs, knt, kns, vnt, vns, cache_seqlens, ot, os, lse, ws, H, N_max, D, \
-                     S, C, scale_log2)
+  // Workspace: arrival words, then the partials (S > 1 only).
+  u64* arrive = static_cast<u64*>(workspace);
+  float* ws = S > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + ab) : nullptr;
+  const u64 tag = S > 1 ? next_tag() : 0;
+  const dim3 grid((unsigned)(bh * S));
+#define TFGFA_DECODE_LAUNCH_W(kDP, kMask, kW)                                                     \
+  hipLaunchKernelGGL((decode_kernel<DShape<T, kDP, kMask>, kW>), grid, dim3(64 * kW), 0, stream, \
+                     qt, qs, kc, ks, vc, vs, knt, kns, vnt, vns, cache_seqlens, ot, os, lse, ws,   \
+                     arrive, tag, H, N_max, D, S, C, scale_log2)
+#define TFGFA_DECODE_LAUNCH(kDP, kMask)                 \
+  do {                                                  \
+    if (S > 1)                                          \
+      TFGFA_DECODE_LAUNCH_W(kDP, kMask, kWavesSplit);   \
+    else                                                \
+      TFGFA_DECODE_LAUNCH_W(kDP, kMask, kWavesWhole);   \
+  } while (0)
   if (D == 64)
     TFGFA_DECODE_LAUNCH(2, false);
   else if (D < 64)
@@ -784,22 +911,9 @@ static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
   else
     TFGFA_DECODE_LAUNCH(4, true);
 #undef TFGFA_DECODE_LAUNCH
-  hipError_t e = hipGetLastError();
+#undef TFGFA_DECODE_LAUNCH_W
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return -(int)e;
-  if (S > 1) {
-    const int heads_per_wg = kMergeThreads / 64;
-    const dim3 mgrid((unsigned)((bh + heads_per_wg - 1) / heads_per_wg));
-    if (D > 64)
-      hipLaunchKernelGGL((decode_merge_kernel<T, true>), mgrid, dim3(kMergeThreads), 0, stream,
-                         static_cast<const float*>(workspace), cache_seqlens, ot, os, lse, (int)bh,
-                         H, N_max, D, S, append);
-    else
-      hipLaunchKernelGGL((decode_merge_kernel<T, false>), mgrid, dim3(kMergeThreads), 0, stream,
-                         static_cast<const float*>(workspace), cache_seqlens, ot, os, lse, (int)bh,
-                         H, N_max, D, S, append);
-    e = hipGetLastError();
-    if (e != hipSuccess) return -(int)e;
-  }
   return TFGFA_OK;
 }
 
@@ -811,7 +925,7 @@ extern "C" size_t tfgfa_decode_workspace_size(int B, int H, int N_max, int D) {
   // One partial per 128 cache rows: an upper bound on the splits of any block size >= 128,
   // so the size does not change with the kernel's tiling.
   const size_t blocks = ((size_t)N_max + kWorkspaceRows - 1) / kWorkspaceRows;
-  return split_bytes((long long)B * H, D) * blocks;
+  return arrive_bytes((long long)B * H) + split_bytes((long long)B * H, D) * blocks;
 }
 
 extern "C" size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max) {

@@ -239,8 +239,10 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     equals the last row of the causal forward over the first L tokens - what the reference's
     generate() recomputes from scratch for every token (src/py/model_inference.py:199-228).
     A length that does not fit the cache yields NaN for that batch row (checked on the device).
-    ``workspace``: optional uint8 device buffer for split-sequence partials (no initialisation
-    needed; an empty one runs each head as one workgroup); when absent, a buffer of
+    ``workspace``: optional uint8 device buffer for split-sequence work (per-head arrival words,
+    then partials; no initialisation needed: each call installs its own random tag in the
+    words and leaves them at zero; an empty buffer runs each head as one workgroup); when
+    absent, a buffer of
     ``_C.decode_workspace_size(B, H, N_max, D)`` bytes is kept per device and stream and reused
     by eager calls.  A call made while the current stream is being captured into a graph gets
     a buffer of its own instead (allocated in the capture, never cached).
@@ -309,14 +311,17 @@ _WORKSPACES: dict = {}
 
 def _decode_workspace(dev, nbytes: int) -> torch.Tensor:
     """A decode workspace of at least ``nbytes`` for (device, current stream), reused across
-    eager calls: it holds only the partials of one call, and calls on one stream do not overlap.
+    eager calls: it holds only the arrival words and partials of one call, and calls on one
+    stream do not overlap.
 
     Under graph capture a fresh buffer is returned and not cached.  A cached one would be
     shared by the graph's replays and by later eager calls on the capture stream (a replay
     racing an eager call on another stream would mix their partials), and a graph would keep
     using the pool block of an entry that a later, larger request replaced.  The fresh buffer
     comes from the capture's memory pool and is released after the call like any temporary of
-    a captured region: the replay uses it in stream order."""
+    a captured region: the replay uses it in stream order.  Later work of the same graph may
+    reuse that memory; the next replay's call still needs no initialisation (its own tag
+    replaces whatever the arrival words then hold)."""
     if torch.cuda.is_current_stream_capturing():
         return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     key = (dev, torch.cuda.current_stream(dev).cuda_stream)
