@@ -17,6 +17,8 @@ after a warm-up of at least 0.1 s, whatever --steps and --warmup say.
 
 Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 2000] [--no-cpu-baseline] [--no-strided]
                       [--no-decode] [--no-generate] [--no-configs]
+       python bench.py --profile WORKLOAD [--launches 15]   (a bounded run for rocprofv3 --pmc)
+       python bench.py --calibrate-copy MIB                 (copy kernels of known bytes)
 """
 import argparse
 import json
@@ -39,6 +41,30 @@ PEAK_HBM_GBS = 8000.0
 N_SETS = 4
 WARM_S = 0.1        # launches before any timing: clocks settle within ~0.1 s of back-to-back work
 MIN_PER_CALL = 200  # per-launch timings behind every median
+
+
+class BenchConfig:
+    """One of BASELINE.json's attention configs 1-4 as the GPU legs run it: shape, input
+    distribution (Q, K ~ N(0, sigma_qk^2), V ~ N(0, sigma_v^2), bf16) and the seed of its
+    inputs.  The same table as the test oracle's (a CPU test checks they agree); kept here so
+    that the timed legs import nothing from the oracle."""
+
+    def __init__(self, name, b, h, n, d, sigma_qk, sigma_v, seed):
+        self.name, self.B, self.H, self.N, self.D = name, b, h, n, d
+        self.sigma_qk, self.sigma_v, self.seed = sigma_qk, sigma_v, seed
+        self.scale = 1.0 / math.sqrt(d)
+        # algorithmic FLOPs (causal convention 4*B*H*N^2*d / 2) and HBM bytes (bf16 Q, K, V
+        # read, O written, fp32 LSE written)
+        self.flops = 4.0 * b * h * n * n * d / 2.0
+        self.bytes = 2.0 * 4 * b * h * n * d + 4.0 * b * h * n
+
+
+BENCH_CONFIGS = {
+    "config1": BenchConfig("config1", 1, 12, 256, 64, 1.0, 1.0, 1001),
+    "config2": BenchConfig("config2", 8, 12, 1024, 64, 1.0, 1.0, 1002),
+    "config3": BenchConfig("config3", 8, 25, 1024, 64, 3.0, 1.0, 1003),
+    "config4": BenchConfig("config4", 1, 16, 8192, 64, 1.0, 1.0, 1004),
+}
 
 
 def _warm(step, seconds=WARM_S, min_calls=10):
@@ -479,7 +505,6 @@ def time_configs(dev):
     import torch
 
     from custom_flash_attn import _C
-    from oracle import CONFIGS
 
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
@@ -487,7 +512,7 @@ def time_configs(dev):
     legs = [("config1", True), ("config2", True), ("config3", True), ("config3_o_only", False),
             ("config4", True)]
     for leg, with_lse in legs:
-        cfg = CONFIGS[leg.split("_")[0]]
+        cfg = BENCH_CONFIGS[leg.split("_")[0]]
         gen = torch.Generator(device=dev).manual_seed(cfg.seed)
         sets = []
         for _ in range(CONFIG_SETS[cfg.name]):
@@ -530,6 +555,73 @@ def time_configs(dev):
     return out
 
 
+PROFILE_WORKLOADS = ("config1", "config2", "config3", "config3_o_only", "config4", "decode",
+                     "decode_split_B1_H25_L1024", "decode_split_B1_H16_L8192")
+
+
+def profile_workload(dev, name, launches):
+    """A bounded run for counter collection (rocprofv3 --pmc reads counters per dispatch, so the
+    timed legs' tens of thousands of launches are too many): 3 warm-up launches, then exactly
+    `launches` launches of one workload, inputs as in its bench leg (seeded, rotating sets)."""
+    import torch
+
+    from custom_flash_attn import _C
+
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    gen = torch.Generator(device=dev)
+    if name.startswith("config"):
+        cfg = BENCH_CONFIGS[name.split("_")[0]]
+        with_lse = not name.endswith("o_only")
+        gen.manual_seed(cfg.seed)
+        sets = []
+        for _ in range(CONFIG_SETS[cfg.name]):
+            q, k, v = ((torch.randn(cfg.B, cfg.H, cfg.N, cfg.D, device=dev, generator=gen) * sg)
+                       .to(torch.bfloat16) for sg in (cfg.sigma_qk, cfg.sigma_qk, cfg.sigma_v))
+            sets.append((q, k, v, torch.empty_like(q),
+                         torch.empty(cfg.B, cfg.H, cfg.N, device=dev, dtype=torch.float32)))
+
+        def step(i):
+            q, k, v, o, lse = sets[i % len(sets)]
+            _C.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                   lse.data_ptr() if with_lse else 0, cfg.B, cfg.H, cfg.N, cfg.D, cfg.scale, True, sh)
+        shape = f"B{cfg.B} H{cfg.H} N{cfg.N} d{cfg.D}, {'O + LSE' if with_lse else 'O'}"
+    else:
+        if name == "decode":
+            b, h, n, append = B, H, N, True
+        else:
+            b, h, n = (int(x[1:]) for x in name.split("_")[2:])
+            append = False
+        gen.manual_seed(4011)
+        nsets = max(2, -(-600_000_000 // (2 * b * h * n * D * 2)))
+        sets = [((torch.randn(b, h, n, D, device=dev, generator=gen) * SIGMA_QK).to(torch.bfloat16),
+                 torch.randn(b, h, n, D, device=dev, generator=gen).to(torch.bfloat16)) for _ in range(nsets)]
+        q, kn, vn = ((torch.randn(b, h, D, device=dev, generator=gen) * s).to(torch.bfloat16)
+                     for s in (SIGMA_QK, SIGMA_QK, SIGMA_V))
+        seqlens = torch.full((b,), n - 1 if append else n, dtype=torch.int32, device=dev)
+        o = torch.empty(b, h, D, device=dev, dtype=torch.bfloat16)
+        lse = torch.empty(b, h, device=dev, dtype=torch.float32)
+        ws_bytes = _C.decode_workspace_bytes(b, h, n)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        z3 = (0, 0, 0)
+
+        def step(i):
+            kc, vc = sets[i % nsets]
+            _C.decode(q.data_ptr(), q.stride(), kc.data_ptr(), kc.stride(), vc.data_ptr(), vc.stride(),
+                      kn.data_ptr() if append else 0, kn.stride() if append else z3,
+                      vn.data_ptr() if append else 0, vn.stride() if append else z3,
+                      seqlens.data_ptr(), o.data_ptr(), o.stride(), lse.data_ptr(), b, h, n, D, SCALE,
+                      ws.data_ptr(), ws_bytes, sh)
+        shape = (f"B{b} H{h} cache {n} rows{' (last row appended)' if append else ''}, d{D}, "
+                 f"{nsets} rotating caches")
+    for i in range(3):
+        step(i)
+    torch.cuda.synchronize()
+    for i in range(launches):
+        step(3 + i)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": name, "shape": shape, "launches": launches, "warmup_launches": 3}))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -552,6 +644,11 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 5 fp32->bf16 copy kernels over MIB MiB "
                          "(known bytes, for scaling the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--profile", default=None, metavar="W[,W...]",
+                    help="instead of the benchmark, run --launches launches of each listed "
+                         f"workload ({', '.join(PROFILE_WORKLOADS)}), one after the other "
+                         "(for rocprofv3 --pmc, which reads counters per dispatch)")
+    ap.add_argument("--launches", type=int, default=15)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -580,6 +677,15 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"kernel": "bfloat16_copy_kernel", "bytes_read": n * 4,
                           "bytes_written": n * 2, "copies": 5}))
+        return
+    if args.profile:
+        names = args.profile.split(",")
+        bad = [n for n in names if n not in PROFILE_WORKLOADS]
+        if bad:
+            print(f"bench.py: unknown --profile workload(s) {bad}", file=sys.stderr)
+            sys.exit(2)
+        for name in names:
+            profile_workload(dev, name, args.launches)
         return
     info = custom_flash_attn.device_info()
 
