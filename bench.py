@@ -650,6 +650,11 @@ def main():
                          "(for rocprofv3 --pmc, which reads counters per dispatch)")
     ap.add_argument("--launches", type=int, default=15)
     args = ap.parse_args()
+    if args.profile:
+        bad = [n for n in args.profile.split(",") if n not in PROFILE_WORKLOADS]
+        if bad:
+            print(f"bench.py: unknown --profile workload(s) {bad}", file=sys.stderr)
+            sys.exit(2)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the path shards over (batch, head) with no exchange; one GPU's share is what "
@@ -679,12 +684,7 @@ def main():
                           "bytes_written": n * 2, "copies": 5}))
         return
     if args.profile:
-        names = args.profile.split(",")
-        bad = [n for n in names if n not in PROFILE_WORKLOADS]
-        if bad:
-            print(f"bench.py: unknown --profile workload(s) {bad}", file=sys.stderr)
-            sys.exit(2)
-        for name in names:
+        for name in args.profile.split(","):
             profile_workload(dev, name, args.launches)
         return
     info = custom_flash_attn.device_info()

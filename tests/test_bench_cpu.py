@@ -37,3 +37,10 @@ def test_bench_refuses_more_than_one_gpu():
                        timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_bench_rejects_unknown_profile_workload_before_touching_the_gpu():
+    r = subprocess.run([sys.executable, BENCH, "--profile", "config3,config9"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "config9" in r.stderr

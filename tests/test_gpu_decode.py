@@ -8,7 +8,9 @@ mean|dO| <= 2e-3, max|dLSE| <= 1e-3, on Q, K ~ N(0, 3^2) (wide logits) and V ~ N
 Covered: ragged lengths (1 .. N_max), the fused append of the new token (cache row written,
 nothing else touched), the split-sequence path against the one-workgroup path, strided
 caches and views (bitwise equal to contiguous ones), long caches, L = 0, invalid lengths
-(NaN for that row only, nothing appended), agreement with the forward kernel's last row.
+(NaN for that row only, nothing appended), agreement with the forward kernel's last row, and
+the split step's arrival words: garbage or foreign tags replaced, zero after every call,
+split steps of several shapes interleaved on one workspace and replayed from a graph.
 """
 import sys
 
@@ -282,3 +284,64 @@ def test_split_arrival_words_end_at_zero_whatever_they_held():
         assert torch.equal(again[0].view(torch.int16), first[0].view(torch.int16)), hex(held)
         assert torch.equal(again[1], first[1]), hex(held)
         assert torch.equal(words, torch.zeros_like(words)), (hex(held), words)
+
+
+def test_split_steps_interleaved_on_one_workspace_and_graph_replayed():
+    """The arrival protocol under load: split steps of three shapes (every head split over
+    several workgroups, the last to arrive merging) run eight times each, interleaved, on one
+    shared workspace.  The shapes differ in B*H, so one shape's partials overlap another's
+    arrival words: every call also meets words holding foreign data and must install its own
+    tag.  Then six steps (two per shape) are captured into one graph and replayed five times
+    with eager steps on the same workspace in between.  Every result is bitwise the result of
+    a call with a fresh workspace, which itself matches the oracle."""
+    shapes = [(1, 4, 4096, 501), (1, 16, 8192, 502), (2, 6, 2048, 503)]
+    cases, refs = [], []
+    for B, H, N_max, seed in shapes:
+        q, kc, vc = _case(B, H, N_max, seed)
+        lens = [N_max - 3 - 5 * b for b in range(B)]
+        sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+        qd, kd, vd = _dev(q), _dev(kc), _dev(vc)
+        fresh = torch.empty(_C.decode_workspace_bytes(B, H, N_max), dtype=torch.uint8, device=DEV)
+        o, l = custom_flash_attn.decode(qd, kd, vd, sl, return_lse=True, workspace=fresh)
+        torch.cuda.synchronize()
+        o_ref, l_ref = decode_np(q, kc, vc, lens, 0.125)
+        _check(o, l, o_ref, l_ref, f"split B={B} H={H} L={N_max}")
+        cases.append((qd, kd, vd, sl))
+        refs.append((o.clone(), l.clone()))
+    nbytes = max(_C.decode_workspace_bytes(B, H, N) for B, H, N, _ in shapes)
+    ws = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=DEV)
+
+    def same(i, o, l, label):
+        assert torch.equal(o.view(torch.int16), refs[i][0].view(torch.int16)), label
+        assert torch.equal(l, refs[i][1]), label
+
+    for rep in range(8):
+        outs = [custom_flash_attn.decode(*cases[i], return_lse=True, workspace=ws)
+                for i in (rep % 3, (rep + 1) % 3, (rep + 2) % 3)]
+        torch.cuda.synchronize()
+        for k, (o, l) in enumerate(outs):
+            same((rep + k) % 3, o, l, f"eager rep {rep} call {k}")
+    _say("interleaved eager split steps: 24 calls bitwise equal")
+
+    outs = [(torch.empty_like(refs[j % 3][0]), torch.empty_like(refs[j % 3][1])) for j in range(6)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for j in range(6):
+                o, l = custom_flash_attn.decode(*cases[j % 3], return_lse=True, workspace=ws)
+                outs[j][0].copy_(o)
+                outs[j][1].copy_(l)
+    torch.cuda.current_stream().wait_stream(side)
+    for rep in range(5):
+        for o, l in outs:
+            o.fill_(float("nan"))
+            l.fill_(float("nan"))
+        graph.replay()
+        eager = custom_flash_attn.decode(*cases[rep % 3], return_lse=True, workspace=ws)
+        torch.cuda.synchronize()
+        for j, (o, l) in enumerate(outs):
+            same(j % 3, o, l, f"replay {rep} step {j}")
+        same(rep % 3, *eager, f"eager after replay {rep}")
+        _say(f"graph replay {rep}: 6 split steps bitwise equal")
