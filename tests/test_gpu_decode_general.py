@@ -10,7 +10,8 @@ Covered per element type (bf16, fp16) and head dim (8, 40, 64, 96, 128): ragged 
 the fused append (cache row written, nothing else touched), the split-sequence path against
 the one-workgroup path, strided caches (bitwise equal to contiguous ones), NaN rows for
 invalid lengths, NaN / inf in cache rows past the length (no effect); and bf16 / D = 64
-bitwise equal to the bf16 entry point.
+bitwise equal to the bf16 entry point.  At D = 96 and 128, both sides of the split threshold
+(B*H at half the CUs splits, one head more does not).
 """
 import sys
 
@@ -121,6 +122,31 @@ def test_split_and_single_workgroup_paths_agree(dt, D):
     o_ref, l_ref = decode_np(q, kc, vc, [L], D ** -0.5)
     _check(split[0], split[1], o_ref, l_ref, f"{dt} D={D} split")
     _check(single[0], single[1], o_ref, l_ref, f"{dt} D={D} single workgroup")
+
+
+@pytest.mark.parametrize("D", [96, 128])
+def test_split_threshold_at_half_the_cus(D):
+    """Heads are split while B*H is at most half the CUs, and run one workgroup each above.
+    The split path leaves its arrival words (64-bit, 128 bytes apart at the workspace start)
+    at zero; the unsplit path never touches the workspace.  Both sides of the threshold
+    against the oracle (fp16, ragged lengths)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    N_max = 1024
+    for B, H, splits in ((2, cus // 4, True), (1, cus // 2 + 1, False)):
+        lens = [N_max - 1 - 37 * b for b in range(B)]
+        _say(f"decode threshold D={D} B={B} H={H} lens={lens} split={splits}")
+        q, kc, vc = _case(B, H, N_max, D, 300 + D + H, "f16")
+        sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+        ws = torch.full((_C.decode_workspace_size(B, H, N_max, D),), 0x5A, dtype=torch.uint8,
+                        device=DEV)
+        o, lse = custom_flash_attn.decode(_dev(q, "f16"), _dev(kc, "f16"), _dev(vc, "f16"), sl,
+                                          return_lse=True, workspace=ws)
+        torch.cuda.synchronize()
+        words = ws[: B * H * 128].view(torch.int64)[::16]
+        expect = 0 if splits else int.from_bytes(b"\x5a" * 8, "little")
+        assert torch.equal(words, torch.full_like(words, expect)), (B, H, words[:4])
+        o_ref, l_ref = decode_np(q, kc, vc, lens, D ** -0.5)
+        _check(o, lse, o_ref, l_ref, f"f16 D={D} B*H={B * H}")
 
 
 @pytest.mark.parametrize("D", [40, 96])

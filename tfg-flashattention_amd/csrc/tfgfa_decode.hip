@@ -16,7 +16,7 @@
 //
 // Work decomposition (split over the cache sequence)
 //   grid = B * H * S workgroups of kW waves; workgroup (bh, s) covers keys [s*C, s*C + C) of
-//   head bh.  S = 1 (8-wave workgroups, one per head) while B*H covers at least half the CUs;
+//   head bh.  S = 1 (8-wave workgroups, one per head) while B*H exceeds half the CUs; at or
 //   below that the host splits each head over 4-wave workgroups that fill one round of
 //   workgroup slots (choose_split).  Inside a workgroup, wave w takes 32-key blocks w, w+kW,
 //   w+2kW, ... of the chunk.
@@ -685,8 +685,12 @@ __global__ __launch_bounds__(64 * kW) void decode_kernel(
 
 // Splits for a cache of N_max rows of head dim D.  One 8-wave workgroup per head keeps 128 KiB
 // of K/V loads in flight, enough to stream at HBM rate from one CU, so heads are not split
-// while B*H covers at least half the CUs (no partials, no arrival count; measured: two splits
-// per head at B*H = 200 cost 30% more).  Below that, a head is split over 4-wave workgroups,
+// while B*H exceeds half the CUs (no partials, no arrival count).  Measured (graph-replayed
+// steps, us, unsplit -> split): 8 x 25 x 1024, D = 64: 11.97 -> 14.47; 16 x 12 x 1024, D = 128:
+// 22.03 -> 25.47; at exactly half the CUs (B*H = 128) 4 x 32 x 2048, D = 64: 15.93 -> 15.83,
+// 8 x 16 x 1024, D = 128: 17.13 -> 16.64 and 2 x 64 x 2048, D = 96: 27.48 -> 22.65 (one
+// 222-VGPR workgroup per CU above D = 64, so half the CUs idle unsplit).  At or below half the
+// CUs a head is split over 4-wave workgroups,
 // two per CU, rounding down so that no slot runs two, and no split holds less than
 // kSplitBytes of K and V (one key block at least).  Measured (graph-replayed steps, caches
 // rotating through HBM; two-kernel split with 8-wave workgroups -> this one-kernel split):
@@ -700,7 +704,7 @@ constexpr int kSplitSlotsPerCu = 2;
 static void choose_split(int BH, int N_max, int D, int cu_count, int max_splits, int* S_out,
                          int* C_out) {
   const int sblocks = std::max(1, (N_max + kSplitBlockKeys - 1) / kSplitBlockKeys);
-  if (2 * BH < cu_count && sblocks >= kMinSplitBlocks) {
+  if (2 * BH <= cu_count && sblocks >= kMinSplitBlocks) {
     int S = std::max(1, kSplitSlotsPerCu * cu_count / BH);
     const int split_keys = std::max(kSplitBlockKeys, kSplitBytes / (4 * D));
     S = std::min(S, (N_max + split_keys - 1) / split_keys);
