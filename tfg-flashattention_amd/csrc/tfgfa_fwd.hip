@@ -99,12 +99,14 @@ constexpr int kMaxD = 128;
 constexpr int kOutOfRange = 0x7FFFFFF0;
 
 // The exp2 offset m of a row moves (to the row's exact running max, rescaling O and the sums)
-// only when the probabilities grow too large: for bf16 in a full half-step, when a lane's sum
-// of its rounded probabilities passes 2^64; otherwise (fp16, and a wave's last half-step),
-// when some score exceeds m by more than the type's margin (64 / 15 log2 units).  So P stays bounded and the rescale is rare.  O is normalised by l_p, the sum of the
-// probabilities *as rounded* for the P.V MFMA, so the rounding of a dominant probability
-// cancels between O's numerator and denominator; the LSE uses l_run, the fp32 sum of the
-// unrounded ones.
+// only when the probabilities grow too large: for bf16 in a full half-step, when a lane's running
+// sum of its rounded probabilities would pass 2^64; otherwise (fp16, and a wave's last
+// half-step), when some score exceeds m by more than the type's margin (60 / 15 log2 units).
+// So P stays bounded and the rescale is rare.  For bf16 a lane's probabilities sum to at most
+// 2^64 through the full half-steps and its last half adds at most 16 * 2^60 = 2^64, so each P.V
+// accumulator stays below 2^66 * max|V|.  O is normalised by l_p, the sum of the probabilities
+// *as rounded* for the P.V MFMA, so the rounding of a dominant probability cancels between O's
+// numerator and denominator; the LSE uses l_run, the fp32 sum of the unrounded ones.
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -120,10 +122,11 @@ struct Elem<__bf16> {
   static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  // Offset margin (log2 units): P <= 2^64 keeps the fp32 sums finite for |V| * N < 2^64.
-  static constexpr float kMargin = 64.0f;
-  // Bound on a half's probability sum in the fused half-step's offset check (every P of the
-  // half is at most the sum): the margin's bound.
+  // Offset margin (log2 units) of the lane-max check of a wave's last half: P <= 2^60, so the
+  // lane's 16 probabilities of that half sum to at most 2^64.
+  static constexpr float kMargin = 60.0f;
+  // Bound on a lane's running probability sum in the fused half-step's offset check (every P
+  // so far is at most the sum).
   static constexpr float kSumBound = 0x1p64f;
   // acc + the sum of the 8 elements of p (exact products by 1, fp32 accumulation).
   static __device__ __forceinline__ float sum8(v8 p, float acc) {
@@ -250,24 +253,52 @@ struct Shape {
 // 1-KiB LDS blocks per dim half (dim half dh at byte dh * 8 KiB of the slot).  Lane i of a block
 // fills physical chunk i%8 of row i/8, so it fetches the logical chunk that the swizzle maps
 // there: head dims 64*dh + 8*chunk .. +7, i.e. row bytes 128*dh + 16*chunk.
-template <class Sh, bool kIsV>
-__device__ __forceinline__ void issue_half(i32x4 desc, int row_bytes, unsigned char* dst, int k0,
-                                           int wave, int lane, int d_chunks) {
+// The lane's byte offset within a tile (from the tile's first row) is the same for every tile,
+// so it is computed once (tile_offsets); per tile only the descriptor moves (tile_desc), in
+// scalar registers, and the transfers take no VALU work.
+template <class Sh>
+__device__ __forceinline__ void tile_offsets(int (*koff)[2], int (*voff)[2], int k_row_bytes,
+                                             int v_row_bytes, int wave, int lane, int d_chunks) {
 #pragma unroll
   for (int dh = 0; dh < Sh::kDH; ++dh)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int blk = 2 * wave + i;
-      const int row = blk * 8 + (lane >> 3);
-      const int pc = lane & 7;
-      const int sw = kIsV ? swz_v(row) : swz_k(row);
-      const int chunk = 8 * dh + (pc ^ sw);  // 16-B chunk of the row in memory
-      // Uniform part (first row of the block) in a scalar register, per-lane part in a vector one.
-      const int s_off = __builtin_amdgcn_readfirstlane((k0 + blk * 8) * row_bytes);
-      int off = s_off + ((lane >> 3) * row_bytes + (chunk << 4));
-      if (Sh::kMaskD) off = chunk < d_chunks ? off : kOutOfRange;
-      lds_transfer(desc, lds_addr(dst + dh * kHalfTileBytes + blk * 1024), off);
+      const int row = (2 * wave + i) * 8 + (lane >> 3);
+      const int kc = 8 * dh + ((lane & 7) ^ swz_k(row));  // 16-B chunk of the row in memory
+      const int vc = 8 * dh + ((lane & 7) ^ swz_v(row));
+      int ko = row * k_row_bytes + (kc << 4);
+      int vo = row * v_row_bytes + (vc << 4);
+      if (Sh::kMaskD) {
+        ko = kc < d_chunks ? ko : kOutOfRange;
+        vo = vc < d_chunks ? vo : kOutOfRange;
+      }
+      koff[dh][i] = ko;
+      voff[dh][i] = vo;
     }
+}
+
+// The head's descriptor moved to row k0: base + k0 rows, num_records reduced by as much, so a
+// row at or past the sequence end still reads zero.  k0 < N for every tile issued.
+__device__ __forceinline__ i32x4 tile_desc(i32x4 desc, int k0, int row_bytes) {
+  const uint32_t adv = (uint32_t)(k0 * row_bytes);
+  const uint64_t base = ((uint64_t)(uint32_t)desc[1] << 32 | (uint32_t)desc[0]) + adv;
+  i32x4 d;
+  d[0] = (int)(uint32_t)base;
+  d[1] = (int)(uint32_t)(base >> 32);
+  d[2] = desc[2] - (int)adv;
+  d[3] = desc[3];
+  return d;
+}
+
+template <class Sh>
+__device__ __forceinline__ void issue_tile(i32x4 desc, int row_bytes, unsigned char* dst, int k0,
+                                           int wave, const int (*off)[2]) {
+  const i32x4 d = tile_desc(desc, k0, row_bytes);
+#pragma unroll
+  for (int dh = 0; dh < Sh::kDH; ++dh)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      lds_transfer(d, lds_addr(dst + dh * kHalfTileBytes + (2 * wave + i) * 1024), off[dh][i]);
 }
 
 // Workgroup barrier that is also a compiler memory barrier: no LDS access moves across it (the
@@ -455,14 +486,16 @@ __device__ __forceinline__ typename Elem<typename Sh::T>::v8 k_operand(const Wav
 //                    P_u = exp2(scale*log2e*S_u - m_run)
 //   chunks kPv+1..   MFMA i of S_{u+1} = K_{u+1} Q^T, the next operand read, a share of
 //                    the sums of P_u and its conversion to the element type
-// The offset check (bf16) reads the sum of the half's probabilities as rounded to the element
-// type: a rounded P above 2^64 makes that sum exceed it (an overflow gives +inf, a -inf offset
-// on a wave's first half gives +inf or NaN), so a sum above the bound, or not a number, takes
-// the rare branch: move the offset to the rows' exact running max, rescale O and the sums,
-// recompute P_u.  A sum above the bound without any single P above it moves the offset early,
-// which is harmless.  fp16 checks the lane max of the scores against the margin instead, in
-// chunk 0, and takes the same branch.
-template <class Sh, int kVs, int kVh, int kKs, int kKh>
+// The offset check (bf16) reads the lane's running sum l_p with this half's probabilities, as
+// rounded to the element type, added: a rounded P above 2^64 makes that sum exceed it (an
+// overflow gives +inf, a -inf offset on a wave's first half gives +inf or NaN), so a sum above
+// the bound, or not a number, takes the rare branch: move the offset to the rows' exact running
+// max, rescale O and the sums, recompute P_u.  A sum above the bound without any single P above
+// it moves the offset early, which is harmless (after a move every P is at most 1, so l_p stays
+// below the number of keys).  So l_p, and with it every P and |O| / max|V|, stays at most 2^64.
+// fp16 checks the lane max of the scores against the margin instead, in chunk 0, and takes the
+// same branch.
+template <class Sh, int kVs, int kVh, int kKs, int kKh, bool kPV = true>
 __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, float scale_log2,
                                            float inv_scale_log2) {
   typedef typename Sh::T T;
@@ -471,8 +504,10 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
   constexpr int kS = 4 * Sh::kDH;
   constexpr float kSumBound = Elem<T>::kSumBound;
   v8 vop[2];
-  vop[0] = v_operand<Sh, kVs, kVh>(w, lds, 0);
-  vop[1] = v_operand<Sh, kVs, kVh>(w, lds, 1);
+  if constexpr (kPV) {
+    vop[0] = v_operand<Sh, kVs, kVh>(w, lds, 0);
+    vop[1] = v_operand<Sh, kVs, kVh>(w, lds, 1);
+  }
   // fp16 keeps the lane-max check (a score more than the margin above the offset): its sum
   // bound is tight enough that the sum check moved the offset more often.
   constexpr bool kMaxCheck = std::is_same<T, _Float16>::value;
@@ -489,11 +524,12 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
 #pragma unroll
   for (int i = 0; i < kPv; ++i) {
     const int dh = i >> 2, cc = (i >> 1) & 1, dt = i & 1;
-    w.o[2 * dh + dt] = Elem<T>::mfma(vop[i & 1], w.pb[cc], w.o[2 * dh + dt]);
-    if (i + 2 < kPv)
-      vop[i & 1] = v_operand<Sh, kVs, kVh>(w, lds, i + 2);
-    else
+    if constexpr (kPV) w.o[2 * dh + dt] = Elem<T>::mfma(vop[i & 1], w.pb[cc], w.o[2 * dh + dt]);
+    if (i + 2 < kPv) {
+      if constexpr (kPV) vop[i & 1] = v_operand<Sh, kVs, kVh>(w, lds, i + 2);
+    } else {
       kop[i + 2 - kPv] = k_operand<Sh, kKs, kKh>(w, lds, i + 2 - kPv);
+    }
 #pragma unroll
     for (int t = 16 * i / kPv; t < 16 * (i + 1) / kPv; ++t)
       p[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, neg_m));
@@ -524,7 +560,10 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
       convert(p);
       asm volatile("" : "+v"(w.pb[0]), "+v"(w.pb[1]));
     } else if (i == 1) {
-      float hs = Elem<T>::sum8(w.pb[0], 0.f) + Elem<T>::sum8(w.pb[1], 0.f);
+      // bf16: the running sum with this half's rounded probabilities added (one of the two
+      // dot2 chains starts from l_p); fp16: the half's own sum.
+      const float l_old = w.l_p;
+      float hs = Elem<T>::sum8(w.pb[0], kMaxCheck ? 0.f : l_old) + Elem<T>::sum8(w.pb[1], 0.f);
       // As unsigned integers, the bits of a sum >= +0 exceed those of the bound exactly when
       // the sum does, is +inf or is a NaN (the device pass assumes no NaN in float compares).
       const bool move = kMaxCheck ? max_move
@@ -545,8 +584,12 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
         for (int t = 0; t < 16; ++t) p[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, -m_new));
         convert(p);
         hs = Elem<T>::sum8(w.pb[0], 0.f) + Elem<T>::sum8(w.pb[1], 0.f);
+        if constexpr (!kMaxCheck) hs += w.l_p;  // l_p already rescaled by alpha
       }
-      w.l_p += hs;
+      if constexpr (kMaxCheck)
+        w.l_p += hs;
+      else
+        w.l_p = hs;
       asm volatile("" : "+v"(w.l_p));
     } else if (i == 2 && Sh::kLse) {
       float s0 = p[0], s1 = p[1];
@@ -568,6 +611,7 @@ struct StepArgs {
   i32x4 k_rsrc, v_rsrc;
   int k_row_bytes, v_row_bytes;  // byte distance between consecutive K (V) rows of a head
   int d_chunks;  // 16-B chunks of a row holding head dims < D
+  int k_lane[2][2], v_lane[2][2];  // this lane's byte offsets within a K / V tile (tile_offsets)
   int nT;        // 64-key tiles loaded by the workgroup
   int nAct;      // 32-key halves this wave computes (a prefix)
   int nFull;     // halves this wave computes without an element mask (a prefix of the above)
@@ -579,19 +623,19 @@ struct StepArgs {
 // slot kKs, half kKh).  kSteady: 1 <= u < nAct - 1 is not required, only u < nAct (a full
 // half-step) - no early exits, so each MFMA group shares a basic block with independent VALU
 // work (P.V with the row max, S_{u+1} with the exponentials):
-//  - u = 0: P is zero and the V slot read was zero-filled, so the P.V adds nothing;
+//  - u = 0 has no P.V before it (kPV = false; the tail path skips it at run time);
 //  - S_{u+1} is computed even past the wave's last half (finite, discarded).
 // Otherwise (tail): u = nAct is the P.V of the last half only; u > nAct does nothing.
-template <class Sh, int kVs, int kVh, int kKs, int kKh, bool kSteady>
+template <class Sh, int kVs, int kVh, int kKs, int kKh, bool kSteady, bool kPV = true>
 __device__ __forceinline__ void half_step(WaveState<Sh>& w, const Lds& lds, int u,
                                           const StepArgs& a) {
   if (!kSteady && u > a.nAct) return;
   if (u >= a.nFull && u < a.nAct) mask_half(w, a.last_key - u * 32 - 4 * a.h);
   if (kSteady) {
-    fused_step<Sh, kVs, kVh, kKs, kKh>(w, lds, a.scale_log2, a.inv_scale_log2);
+    fused_step<Sh, kVs, kVh, kKs, kKh, kPV>(w, lds, a.scale_log2, a.inv_scale_log2);
     return;
   }
-  pv_half<Sh, kVs, kVh>(w, lds);
+  if (u > 0) pv_half<Sh, kVs, kVh>(w, lds);
   const float mx = lane_max(w);
   if (!kSteady && u == a.nAct) return;
   move_offset(w, mx, a.scale_log2, a.inv_scale_log2);
@@ -603,7 +647,7 @@ __device__ __forceinline__ void half_step(WaveState<Sh>& w, const Lds& lds, int 
 // Tile step j (K slot kKs = j % 3, V slot kVs = j % kVSlots): issue K_{j+2} (and, with a 3-slot
 // V ring, V_{j+1}); half-step 2j; wait for K_{j+1} and V_j; barrier; (2-slot V ring: issue
 // V_{j+1}); half-step 2j+1.
-template <class Sh, int kKs, int kVs, bool kSteady>
+template <class Sh, int kKs, int kVs, bool kSteady, bool kFirst = false>
 __device__ __forceinline__ void tile_step(WaveState<Sh>& w, const Lds& lds, int j,
                                           const StepArgs& a) {
   constexpr int kKNext = (kKs + 1) % kStages;
@@ -613,13 +657,13 @@ __device__ __forceinline__ void tile_step(WaveState<Sh>& w, const Lds& lds, int 
   constexpr int kVNext = (kVs + 1) % kVN;        // V_{j+1}
   const bool k2 = j + 2 < a.nT, v1 = j + 1 < a.nT;
   if (k2)
-    issue_half<Sh, false>(a.k_rsrc, a.k_row_bytes, lds.k[kKNext2], (j + 2) * kTileKeys, a.wave,
-                          a.lane, a.d_chunks);
+    issue_tile<Sh>(a.k_rsrc, a.k_row_bytes, lds.k[kKNext2], (j + 2) * kTileKeys, a.wave,
+                   a.k_lane);
   if (kVN == 3 && v1)
-    issue_half<Sh, true>(a.v_rsrc, a.v_row_bytes, lds.v[kVNext], (j + 1) * kTileKeys, a.wave,
-                         a.lane, a.d_chunks);
+    issue_tile<Sh>(a.v_rsrc, a.v_row_bytes, lds.v[kVNext], (j + 1) * kTileKeys, a.wave,
+                   a.v_lane);
   // Half 2j: P.V of half 2j-1 (V_{j-1}, keys 32..63), S of half 2j+1 (K_j, keys 32..63).
-  half_step<Sh, kVPrev, 1, kKs, 1, kSteady>(w, lds, 2 * j, a);
+  half_step<Sh, kVPrev, 1, kKs, 1, kSteady, !kFirst>(w, lds, 2 * j, a);
   // K_{j+1} and V_j were issued by step j-1; only this step's loads may still be in flight.
   if (kVN == 3 && k2 && v1)
     wait_vmcnt<Sh::kLoadsPerWave>();
@@ -629,8 +673,8 @@ __device__ __forceinline__ void tile_step(WaveState<Sh>& w, const Lds& lds, int 
     wait_vmcnt<0>();
   lds_barrier();
   if (kVN == 2 && v1)
-    issue_half<Sh, true>(a.v_rsrc, a.v_row_bytes, lds.v[kVNext], (j + 1) * kTileKeys, a.wave,
-                         a.lane, a.d_chunks);
+    issue_tile<Sh>(a.v_rsrc, a.v_row_bytes, lds.v[kVNext], (j + 1) * kTileKeys, a.wave,
+                   a.v_lane);
   // Half 2j+1: P.V of half 2j (V_j, keys 0..31), S of half 2j+2 (K_{j+1}, keys 0..31).
   half_step<Sh, kVs, 0, kKNext, 0, kSteady>(w, lds, 2 * j + 1, a);
 }
@@ -647,26 +691,26 @@ __device__ __forceinline__ void tile_step_at(WaveState<Sh>& w, const Lds& lds, i
   }
 }
 
-// kPeriod steady tile steps j0 .. j0 + kPeriod - 1 (j0 a multiple of kPeriod), slots at
+// kPeriod steady tile steps j0 .. j0 + kPeriod - 1 (j0 = kJ0 modulo kPeriod), slots at
 // compile time.
-template <class Sh, int kP = 0>
+template <class Sh, int kJ0 = 0, int kP = 0>
 __device__ __forceinline__ void steady_period(WaveState<Sh>& w, const Lds& lds, int j0,
                                               const StepArgs& a) {
   if constexpr (kP < Sh::kPeriod) {
-    tile_step<Sh, kP % kStages, kP % Sh::kVSlots, true>(w, lds, j0 + kP, a);
-    steady_period<Sh, kP + 1>(w, lds, j0, a);
+    tile_step<Sh, (kJ0 + kP) % kStages, (kJ0 + kP) % Sh::kVSlots, true>(w, lds, j0 + kP, a);
+    steady_period<Sh, kJ0, kP + 1>(w, lds, j0, a);
   }
 }
 
-// The steady tile steps j0 .. n - 1 of a partial period (n - j0 < kPeriod), slots at compile
-// time.
-template <class Sh, int kP = 0>
+// The steady tile steps j0 .. n - 1 of a partial period (n - j0 < kPeriod, j0 = kJ0 modulo
+// kPeriod), slots at compile time.
+template <class Sh, int kJ0 = 0, int kP = 0>
 __device__ __forceinline__ void steady_rest(WaveState<Sh>& w, const Lds& lds, int j0, int n,
                                             const StepArgs& a) {
   if constexpr (kP + 1 < Sh::kPeriod) {
     if (j0 + kP < n) {
-      tile_step<Sh, kP % kStages, kP % Sh::kVSlots, true>(w, lds, j0 + kP, a);
-      steady_rest<Sh, kP + 1>(w, lds, j0, n, a);
+      tile_step<Sh, (kJ0 + kP) % kStages, (kJ0 + kP) % Sh::kVSlots, true>(w, lds, j0 + kP, a);
+      steady_rest<Sh, kJ0, kP + 1>(w, lds, j0, n, a);
     }
   }
 }
@@ -764,10 +808,10 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
       w.qop[c] = __builtin_bit_cast(v8, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
     }
   }
-  issue_half<Sh, false>(a.k_rsrc, a.k_row_bytes, lds.k[0], 0, wave, lane, a.d_chunks);
-  if (a.nT > 1)
-    issue_half<Sh, false>(a.k_rsrc, a.k_row_bytes, lds.k[1], kTileKeys, wave, lane, a.d_chunks);
-  issue_half<Sh, true>(a.v_rsrc, a.v_row_bytes, lds.v[0], 0, wave, lane, a.d_chunks);
+  tile_offsets<Sh>(a.k_lane, a.v_lane, a.k_row_bytes, a.v_row_bytes, wave, lane, a.d_chunks);
+  issue_tile<Sh>(a.k_rsrc, a.k_row_bytes, lds.k[0], 0, wave, a.k_lane);
+  if (a.nT > 1) issue_tile<Sh>(a.k_rsrc, a.k_row_bytes, lds.k[1], kTileKeys, wave, a.k_lane);
+  issue_tile<Sh>(a.v_rsrc, a.v_row_bytes, lds.v[0], 0, wave, a.v_lane);
 
   // K A-operand, d chunk c: row r32 (+32 for the second key half, an immediate), logical 16-B
   // chunk 2c + h.
@@ -796,13 +840,6 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   w.l_run = 0.f;
   w.l_p = 0.f;
 
-  // Half-step 0 runs a P.V against the last V slot (that of V_{-1}) with P = 0: zero that
-  // slot so no stale LDS value (possibly NaN) meets the zeros.
-  {
-    uint4* vz = reinterpret_cast<uint4*>(lds.v[Sh::kVSlots - 1]);
-#pragma unroll
-    for (int i = 0; i < kSlotBytes / 16 / kThreads; ++i) vz[tid + i * kThreads] = make_uint4(0u, 0u, 0u, 0u);
-  }
 #pragma unroll
   for (int cc = 0; cc < 2; ++cc) w.pb[cc] = __builtin_bit_cast(v8, make_uint4(0u, 0u, 0u, 0u));
 
@@ -817,12 +854,17 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   lds_barrier();
   if (a.nAct > 0) w.s = qk_half<Sh, 0, 0>(w, lds);
 
-  // Steady tile steps: both half-steps full (2j + 1 < nAct).
+  // Steady tile steps: both half-steps full (2j + 1 < nAct).  Tile step 0's first half-step has
+  // no P.V before it.
   const int nSteady = a.nAct / 2;
   int j = 0;
-  for (; j + Sh::kPeriod <= nSteady; j += Sh::kPeriod) steady_period<Sh>(w, lds, j, a);
-  steady_rest<Sh>(w, lds, j, nSteady, a);
-  j = max(j, nSteady);
+  if (nSteady > 0) {
+    tile_step<Sh, 0, 0, true, true>(w, lds, 0, a);
+    j = 1;
+    for (; j + Sh::kPeriod <= nSteady; j += Sh::kPeriod) steady_period<Sh, 1>(w, lds, j, a);
+    steady_rest<Sh, 1>(w, lds, j, nSteady, a);
+    j = max(j, nSteady);
+  }
   // Remaining tile steps (the wave's last half and P.V, then loads and barriers only).
   for (; j < a.nT; ++j) tile_step_at<Sh, false>(w, lds, j, a);
   // P.V of the last computed half when it is the second half of the last tile (V_{nT-1}
