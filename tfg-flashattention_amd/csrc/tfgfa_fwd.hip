@@ -27,12 +27,14 @@
 //
 // Memory pipeline
 //   K and V tiles go from HBM straight into LDS (buffer_load_dwordx4 ... lds: each lane's
-//   16 B land at LDS base + 16*lane), no registers or VALU spent on staging.  A ring of 3 K
-//   slots and a ring of 3 (head dim 64) or 2 (head dim 128) V slots.  Tile step j: issue
-//   K_{j+2} (and V_{j+1} with 3 V slots); half-step 2j (uses K_j, V_{j-1}); wait for this
-//   wave's loads of K_{j+1} and V_j and barrier; (2 V slots: issue V_{j+1} into V_{j-1}'s
-//   slot); half-step 2j+1 (uses K_{j+1}, V_j).  The barrier also proves every wave has
-//   finished with the slots refilled after it.
+//   16 B land at LDS base + 16*lane), no registers or VALU spent on staging.  A ring of 2
+//   (head dim 64) or 3 (head dim 128) K slots and a ring of 2 V slots.  Tile step j: (3 K
+//   slots: issue K_{j+2}); half-step 2j (uses K_j, V_{j-1}); wait for this wave's loads of
+//   K_{j+1} and V_j and barrier; issue V_{j+1} into V_{j-1}'s slot (2 K slots: and K_{j+2}
+//   into K_j's); half-step 2j+1 (uses K_{j+1}, V_j).  The barrier also proves every wave has
+//   finished with the slots refilled after it.  At head dim 64 the prologue also moves the
+//   wave's Q rows through LDS, so the first S waits for Q and K_0 only (K_1 and V_0 are waited
+//   for in tile step 0).
 //   Loads past the sequence end return zero (buffer range check): the zero-fill of partial
 //   tiles.
 //
@@ -92,7 +94,6 @@ constexpr int kBlockRows = kWaves * kWaveRows;  // 128 query rows per workgroup
 constexpr int kTileKeys = 64;               // keys per K/V tile
 constexpr int kKRowBytes = kDHalf * 2;      // 128 B per key row of one dim half in LDS
 constexpr int kHalfTileBytes = kTileKeys * kKRowBytes;  // 8 KiB (K or V, one dim half)
-constexpr int kStages = 3;  // K ring slots (the V ring has Shape::kVSlots: 3 or 2)
 constexpr int kMaxD = 128;
 // A buffer offset past any num_records built here (those stay below 2^31 - 2^24): the load
 // returns zero without a memory access.  Used for head dims past D when D < the tile's dims.
@@ -238,15 +239,25 @@ struct Shape {
   static constexpr bool kMaskD = kMaskD_;
   typedef T_ T;
   static constexpr int kLoadsPerWave = 4 * kDH;  // transfers per tile step per wave (K and V)
-  // V ring slots.  3: V_{j+1} is issued at the start of tile step j.  2: V_{j+1} is issued after
-  // step j's barrier, into the slot of V_{j-1} (read by half-step 2j, before the barrier); the
-  // rings then take 5 slots of LDS instead of 6.  Head dim 128 uses 2: 80 KiB of LDS per
-  // workgroup, so two workgroups (two waves per SIMD) fit a CU's 160 KiB.
-  static constexpr int kVSlots = kD_ == 128 ? 2 : 3;
+  // K ring slots.  2: K_{j+2} is issued after tile step j's barrier, into the slot of K_j (last
+  // read by half-step 2j, before the barrier), and has two half-steps to land.  3: K_{j+2} is
+  // issued at the start of step j, into the slot of K_{j-1}, and has three.  Head dim 64 uses 2
+  // (as fast, measured, and it leaves LDS for the Q stage); head dim 128 uses 3 (2 was ~3%
+  // slower there).
+  static constexpr int kKSlots = kD_ == 128 ? 3 : 2;
+  // V ring: 2 slots; V_{j+1} is issued after step j's barrier, into the slot of V_{j-1} (read by
+  // half-step 2j, before the barrier).
+  static constexpr int kVSlots = 2;
   // Tile steps after which the K and V slot assignments repeat.
-  static constexpr int kPeriod = kVSlots == 3 ? 3 : 6;
+  static constexpr int kPeriod = kKSlots == 3 ? 6 : 2;
+  // Q reaches its registers through LDS (a 4-KiB stage per wave): the loads are LDS transfers
+  // that the compiler does not track, so the prologue waits for Q and K_0 only.  Head dim 64
+  // (48 KiB of LDS per workgroup with the rings, three workgroups per CU); head dim 128 loads Q
+  // into registers and waits for the whole prologue (its rings take 80 KiB).
+  static constexpr bool kQStage = kD_ == 64;
+  static constexpr int kLdsBytes =
+      (kKSlots + kVSlots) * kDH * kHalfTileBytes + (kQStage ? kBlockRows * kKRowBytes : 0);
   static_assert(kD_ == 64 || kD_ == 128, "compiled head dims");
-  static_assert(kVSlots == 2 || kVSlots == 3, "V ring slots");
 };
 
 // This wave's share of one K (or V) tile: rows [8*(2w), 8*(2w+2)) of each dim half as two
@@ -301,6 +312,26 @@ __device__ __forceinline__ void issue_tile(i32x4 desc, int row_bytes, unsigned c
       lds_transfer(d, lds_addr(dst + dh * kHalfTileBytes + (2 * wave + i) * 1024), off[dh][i]);
 }
 
+// This wave's 32 query rows, from the descriptor's first row, into its 4-KiB LDS stage (head
+// dim 64): row r at byte 128 r, logical 16-B chunk c (head dims 8c .. 8c+7) at physical chunk
+// c ^ swz_k(r), so the 8 (or 16) consecutive rows of one ds_read_b128 hit distinct banks.  Four
+// 1-KiB transfers; rows past the sequence end read zero.
+template <class Sh>
+__device__ __forceinline__ void issue_q_stage(i32x4 qdesc, int row_bytes, unsigned char* dst,
+                                              int d_chunks) {
+  static_assert(Sh::kDH == 1, "the Q stage holds 128-B rows");
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int row = 8 * t + (lane >> 3);
+    const int lc = (lane & 7) ^ swz_k(row);
+    int off = row * row_bytes + (lc << 4);
+    if (Sh::kMaskD) off = lc < d_chunks ? off : kOutOfRange;
+    lds_transfer(qdesc, lds_addr(dst + t * 1024), off);
+  }
+}
+
 // Workgroup barrier that is also a compiler memory barrier: no LDS access moves across it (the
 // s_barrier builtin alone is not a memory operation for the optimizer), and unlike
 // __syncthreads() it adds no wait for outstanding vector memory loads, which would drain the
@@ -314,11 +345,11 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// LDS: a ring of 3 K tiles and a ring of 3 V tiles, each slot its own __shared__ array of kDH
-// dim halves.
+// LDS: a ring of Shape::kKSlots K tiles and a ring of 2 V tiles, each slot kDH dim halves of
+// 8 KiB.
 struct Lds {
-  unsigned char* k[kStages];
-  unsigned char* v[3];
+  unsigned char* k[3];
+  unsigned char* v[2];
 };
 
 // Per-wave state carried across half-steps.
@@ -644,37 +675,35 @@ __device__ __forceinline__ void half_step(WaveState<Sh>& w, const Lds& lds, int 
   w.s = n;
 }
 
-// Tile step j (K slot kKs = j % 3, V slot kVs = j % kVSlots): issue K_{j+2} (and, with a 3-slot
-// V ring, V_{j+1}); half-step 2j; wait for K_{j+1} and V_j; barrier; (2-slot V ring: issue
-// V_{j+1}); half-step 2j+1.
+// Tile step j (K slot kKs = j % kKSlots, V slot kVs = j % 2): (3 K slots: issue K_{j+2});
+// half-step 2j; wait for K_{j+1} and V_j; barrier; issue V_{j+1} (2 K slots: and K_{j+2});
+// half-step 2j+1.
 template <class Sh, int kKs, int kVs, bool kSteady, bool kFirst = false>
 __device__ __forceinline__ void tile_step(WaveState<Sh>& w, const Lds& lds, int j,
                                           const StepArgs& a) {
-  constexpr int kKNext = (kKs + 1) % kStages;
-  constexpr int kKNext2 = (kKs + 2) % kStages;
-  constexpr int kVN = Sh::kVSlots;
-  constexpr int kVPrev = (kVs + kVN - 1) % kVN;  // V_{j-1}
-  constexpr int kVNext = (kVs + 1) % kVN;        // V_{j+1}
+  constexpr int kKN = Sh::kKSlots;
+  constexpr int kKNext = (kKs + 1) % kKN;
+  constexpr int kKNext2 = (kKs + 2) % kKN;  // K_{j-1}'s slot (3 slots), K_j's (2 slots)
+  constexpr int kVOther = kVs ^ 1;          // V_{j-1}, then V_{j+1}
   const bool k2 = j + 2 < a.nT, v1 = j + 1 < a.nT;
-  if (k2)
+  if (kKN == 3 && k2)
     issue_tile<Sh>(a.k_rsrc, a.k_row_bytes, lds.k[kKNext2], (j + 2) * kTileKeys, a.wave,
                    a.k_lane);
-  if (kVN == 3 && v1)
-    issue_tile<Sh>(a.v_rsrc, a.v_row_bytes, lds.v[kVNext], (j + 1) * kTileKeys, a.wave,
-                   a.v_lane);
   // Half 2j: P.V of half 2j-1 (V_{j-1}, keys 32..63), S of half 2j+1 (K_j, keys 32..63).
-  half_step<Sh, kVPrev, 1, kKs, 1, kSteady, !kFirst>(w, lds, 2 * j, a);
-  // K_{j+1} and V_j were issued by step j-1; only this step's loads may still be in flight.
-  if (kVN == 3 && k2 && v1)
-    wait_vmcnt<Sh::kLoadsPerWave>();
-  else if (k2 || (kVN == 3 && v1))
+  half_step<Sh, kVOther, 1, kKs, 1, kSteady, !kFirst>(w, lds, 2 * j, a);
+  // K_{j+1} and V_j were issued by step j-1 (step 0: by the prologue); only K_{j+2}, issued
+  // above with a 3-slot K ring, may stay in flight.
+  if (kKN == 3 && k2)
     wait_vmcnt<Sh::kLoadsPerWave / 2>();
   else
     wait_vmcnt<0>();
   lds_barrier();
-  if (kVN == 2 && v1)
-    issue_tile<Sh>(a.v_rsrc, a.v_row_bytes, lds.v[kVNext], (j + 1) * kTileKeys, a.wave,
+  if (v1)
+    issue_tile<Sh>(a.v_rsrc, a.v_row_bytes, lds.v[kVOther], (j + 1) * kTileKeys, a.wave,
                    a.v_lane);
+  if (kKN == 2 && k2)
+    issue_tile<Sh>(a.k_rsrc, a.k_row_bytes, lds.k[kKNext2], (j + 2) * kTileKeys, a.wave,
+                   a.k_lane);
   // Half 2j+1: P.V of half 2j (V_j, keys 0..31), S of half 2j+2 (K_{j+1}, keys 0..31).
   half_step<Sh, kVs, 0, kKNext, 0, kSteady>(w, lds, 2 * j + 1, a);
 }
@@ -685,7 +714,7 @@ __device__ __forceinline__ void tile_step_at(WaveState<Sh>& w, const Lds& lds, i
                                              const StepArgs& a) {
   if constexpr (kP < Sh::kPeriod) {
     if (j % Sh::kPeriod == kP)
-      tile_step<Sh, kP % kStages, kP % Sh::kVSlots, kSteady>(w, lds, j, a);
+      tile_step<Sh, kP % Sh::kKSlots, kP % Sh::kVSlots, kSteady>(w, lds, j, a);
     else
       tile_step_at<Sh, kSteady, kP + 1>(w, lds, j, a);
   }
@@ -697,7 +726,7 @@ template <class Sh, int kJ0 = 0, int kP = 0>
 __device__ __forceinline__ void steady_period(WaveState<Sh>& w, const Lds& lds, int j0,
                                               const StepArgs& a) {
   if constexpr (kP < Sh::kPeriod) {
-    tile_step<Sh, (kJ0 + kP) % kStages, (kJ0 + kP) % Sh::kVSlots, true>(w, lds, j0 + kP, a);
+    tile_step<Sh, (kJ0 + kP) % Sh::kKSlots, (kJ0 + kP) % Sh::kVSlots, true>(w, lds, j0 + kP, a);
     steady_period<Sh, kJ0, kP + 1>(w, lds, j0, a);
   }
 }
@@ -709,7 +738,7 @@ __device__ __forceinline__ void steady_rest(WaveState<Sh>& w, const Lds& lds, in
                                             const StepArgs& a) {
   if constexpr (kP + 1 < Sh::kPeriod) {
     if (j0 + kP < n) {
-      tile_step<Sh, (kJ0 + kP) % kStages, (kJ0 + kP) % Sh::kVSlots, true>(w, lds, j0 + kP, a);
+      tile_step<Sh, (kJ0 + kP) % Sh::kKSlots, (kJ0 + kP) % Sh::kVSlots, true>(w, lds, j0 + kP, a);
       steady_rest<Sh, kJ0, kP + 1>(w, lds, j0, n, a);
     }
   }
@@ -733,12 +762,12 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   typedef typename Elem<T>::v4 v4;
   constexpr int kSlotBytes = Sh::kDH * kHalfTileBytes;
   constexpr int kDenseRowBytes = Sh::kD * 2;
-  __shared__ __attribute__((aligned(1024))) unsigned char k0s[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char k1s[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char k2s[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char vring[Sh::kVSlots * kSlotBytes];
-  const Lds lds = {{k0s, k1s, k2s},
-                   {vring, vring + kSlotBytes, vring + (Sh::kVSlots - 1) * kSlotBytes}};
+  // K slots, V slots, then (head dim 64) the Q stage: 4 KiB per wave.
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[Sh::kLdsBytes];
+  constexpr int kV0 = Sh::kKSlots * kSlotBytes;
+  constexpr int kQ0 = kV0 + Sh::kVSlots * kSlotBytes;
+  const Lds lds = {{smem, smem + kSlotBytes, smem + (Sh::kKSlots - 1) * kSlotBytes},
+                   {smem + kV0, smem + kV0 + kSlotBytes}};
   const T* Q = static_cast<const T*>(Qv);
   const T* K = static_cast<const T*>(Kv);
   const T* V = static_cast<const T*>(Vv);
@@ -795,10 +824,17 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   a.scale_log2 = scale_log2;
   a.inv_scale_log2 = 1.0f / scale_log2;
 
-  // Q first (ordinary buffer loads, tracked by the compiler), then the prologue tiles K_0, K_1
-  // and V_0 (step j issues K_{j+2} and V_{j+1}).
+  // Q first, then the prologue tiles K_0, K_1 and V_0 (step j issues K_{j+2} and V_{j+1}).
+  // Head dim 64: Q as LDS transfers into this wave's stage.  Head dim 128: ordinary buffer
+  // loads into the Q registers, tracked by the compiler.
   WaveState<Sh> w;
-  {
+  unsigned char* const qstage = smem + kQ0 + wave * (kWaveRows * kKRowBytes);
+  if constexpr (Sh::kQStage) {
+    // A wave past the last query row (q0 >= Nq) computes nothing; its stage reads row Nq - 1.
+    const i32x4 qd = head_desc(Qh, Nq, q_row_bytes);
+    issue_q_stage<Sh>(tile_desc(qd, min(q0, Nq - 1), q_row_bytes), q_row_bytes, qstage,
+                      a.d_chunks);
+  } else {
     const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<T*>(Qh), (short)0, Nq * q_row_bytes, 0x00020000);
 #pragma unroll
@@ -843,15 +879,29 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
 #pragma unroll
   for (int cc = 0; cc < 2; ++cc) w.pb[cc] = __builtin_bit_cast(v8, make_uint4(0u, 0u, 0u, 0u));
 
-  // Wait for Q here, before the loop.  The compiler does not see the LDS transfers, so it
-  // places a full vmcnt(0) before this use of the Q registers; that also covers K_0, K_1 and V_0
-  // (once, in the prologue), and leaves no compiler-tracked loads whose waits could land inside
-  // the loop and drain the transfers in flight there.
+  if constexpr (Sh::kQStage) {
+    // Q and K_0 have landed once K_1 and V_0 (issued after them) are all that may be in flight;
+    // tile step 0 waits for those.  The barrier makes every wave's share of K_0 visible.
+    if (a.nT > 1)
+      wait_vmcnt<Sh::kLoadsPerWave>();
+    else
+      wait_vmcnt<Sh::kLoadsPerWave / 2>();
+    lds_barrier();
 #pragma unroll
-  for (int c = 0; c < 4 * Sh::kDH; ++c) asm volatile("" ::"v"(w.qop[c]));
-  wait_vmcnt<0>();
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  lds_barrier();
+    for (int c = 0; c < 4; ++c)
+      w.qop[c] = *reinterpret_cast<const v8*>(qstage + r32 * kKRowBytes +
+                                              (((2 * c + h) ^ swz_k(r32)) << 4));
+  } else {
+    // Wait for Q here, before the loop.  The compiler does not see the LDS transfers, so it
+    // places a full vmcnt(0) before this use of the Q registers; that also covers K_0, K_1 and
+    // V_0 (once, in the prologue), and leaves no compiler-tracked loads whose waits could land
+    // inside the loop and drain the transfers in flight there.
+#pragma unroll
+    for (int c = 0; c < 4 * Sh::kDH; ++c) asm volatile("" ::"v"(w.qop[c]));
+    wait_vmcnt<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    lds_barrier();
+  }
   if (a.nAct > 0) w.s = qk_half<Sh, 0, 0>(w, lds);
 
   // Steady tile steps: both half-steps full (2j + 1 < nAct).  Tile step 0's first half-step has
@@ -870,13 +920,10 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   // P.V of the last computed half when it is the second half of the last tile (V_{nT-1}
   // landed at the last step's barrier and its slot was not refilled): half-step 2nT.
   if (a.nAct == 2 * a.nT) {
-    const int sl = (a.nT - 1) % Sh::kVSlots;
-    if (sl == 0)
+    if ((a.nT - 1) % Sh::kVSlots == 0)
       pv_half<Sh, 0, 1>(w, lds);
-    else if (sl == 1)
-      pv_half<Sh, 1, 1>(w, lds);
     else
-      pv_half<Sh, 2, 1>(w, lds);
+      pv_half<Sh, 1, 1>(w, lds);
   }
 
   // Row sums over the lane pair (both lanes of a row hold the same offset).
