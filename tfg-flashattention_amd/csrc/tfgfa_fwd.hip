@@ -255,8 +255,6 @@ struct Shape {
   // (48 KiB of LDS per workgroup with the rings, three workgroups per CU); head dim 128 loads Q
   // into registers and waits for the whole prologue (its rings take 80 KiB).
   static constexpr bool kQStage = kD_ == 64;
-  static constexpr int kLdsBytes =
-      (kKSlots + kVSlots) * kDH * kHalfTileBytes + (kQStage ? kBlockRows * kKRowBytes : 0);
   static_assert(kD_ == 64 || kD_ == 128, "compiled head dims");
 };
 
@@ -310,6 +308,14 @@ __device__ __forceinline__ void issue_tile(i32x4 desc, int row_bytes, unsigned c
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       lds_transfer(d, lds_addr(dst + dh * kHalfTileBytes + (2 * wave + i) * 1024), off[dh][i]);
+}
+
+// The workgroup's Q stage (head dim 64): 4 KiB of LDS per wave, allocated only by the instances
+// that call this.
+template <class Sh>
+__device__ __forceinline__ unsigned char* q_stage() {
+  __shared__ __attribute__((aligned(1024))) unsigned char qst[kBlockRows * kKRowBytes];
+  return qst;
 }
 
 // This wave's 32 query rows, from the descriptor's first row, into its 4-KiB LDS stage (head
@@ -762,12 +768,15 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   typedef typename Elem<T>::v4 v4;
   constexpr int kSlotBytes = Sh::kDH * kHalfTileBytes;
   constexpr int kDenseRowBytes = Sh::kD * 2;
-  // K slots, V slots, then (head dim 64) the Q stage: 4 KiB per wave.
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[Sh::kLdsBytes];
-  constexpr int kV0 = Sh::kKSlots * kSlotBytes;
-  constexpr int kQ0 = kV0 + Sh::kVSlots * kSlotBytes;
-  const Lds lds = {{smem, smem + kSlotBytes, smem + (Sh::kKSlots - 1) * kSlotBytes},
-                   {smem + kV0, smem + kV0 + kSlotBytes}};
+  // The V slots first, then the K slots: a ds_read reaches 64 KiB past its base register with
+  // an immediate offset, and at head dim 128 (80 KiB) only the third K slot lies beyond, read by
+  // 8 of a half-step's 24 reads one tile step in three (with the V ring there, half of all
+  // tile steps paid an address add per V read).
+  __shared__ __attribute__((aligned(1024)))
+  unsigned char ring[(Sh::kVSlots + Sh::kKSlots) * kSlotBytes];
+  constexpr int kK0 = Sh::kVSlots * kSlotBytes;
+  const Lds lds = {{ring + kK0, ring + kK0 + kSlotBytes, ring + kK0 + (Sh::kKSlots - 1) * kSlotBytes},
+                   {ring, ring + kSlotBytes}};
   const T* Q = static_cast<const T*>(Qv);
   const T* K = static_cast<const T*>(Kv);
   const T* V = static_cast<const T*>(Vv);
@@ -828,8 +837,9 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   // Head dim 64: Q as LDS transfers into this wave's stage.  Head dim 128: ordinary buffer
   // loads into the Q registers, tracked by the compiler.
   WaveState<Sh> w;
-  unsigned char* const qstage = smem + kQ0 + wave * (kWaveRows * kKRowBytes);
+  unsigned char* qstage = nullptr;
   if constexpr (Sh::kQStage) {
+    qstage = q_stage<Sh>() + wave * (kWaveRows * kKRowBytes);
     // A wave past the last query row (q0 >= Nq) computes nothing; its stage reads row Nq - 1.
     const i32x4 qd = head_desc(Qh, Nq, q_row_bytes);
     issue_q_stage<Sh>(tile_desc(qd, min(q0, Nq - 1), q_row_bytes), q_row_bytes, qstage,
