@@ -44,3 +44,19 @@ def test_bench_rejects_unknown_profile_workload_before_touching_the_gpu():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "config9" in r.stderr
+
+
+def test_bench_traffic_and_bytes_follow_the_instance():
+    """The headline is the drop-in O-only call: its roofline reads the O-only traffic line of the
+    committed counter summary and counts no LSE bytes; the O + LSE leg reads its own line."""
+    bench = _bench()
+    o_only = bench.committed_traffic()
+    with_lse = bench.committed_traffic("traffic_bytes_per_launch")
+    assert o_only is not None and with_lse is not None
+    # measured fabric traffic is at least the algorithmic bytes of each instance
+    assert o_only >= bench.bytes_per_fwd(lse=False)
+    assert with_lse >= bench.bytes_per_fwd(lse=True)
+    B, H, N, D = bench.B, bench.H, bench.N, bench.D
+    assert bench.bytes_per_fwd(lse=False) == 2 * 4 * B * H * N * D
+    assert bench.bytes_per_fwd(lse=True) == 2 * 4 * B * H * N * D + 4 * B * H * N
+    assert bench.committed_traffic("no_such_key") is None
