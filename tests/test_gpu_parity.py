@@ -61,6 +61,13 @@ def _rand(shape, seed, sigma=1.0):
     return (g.standard_normal(shape, dtype=np.float32) * np.float32(sigma))
 
 
+def _gen(seed):
+    """A seeded device generator, so every random draw in these tests is the same on every run."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    return g
+
+
 def _bf(x):
     return torch.from_numpy(x).to(torch.bfloat16).float().numpy()
 
@@ -208,8 +215,8 @@ def test_explicit_scale(scale):
 
 def test_matches_reference_test_vs_sdpa_fp32():
     """test_flash_attention_vs_pytorch (test_cuda_implementation.py:72-91), against SDPA in fp32."""
-    torch.manual_seed(0)
-    q, k, v = (torch.randn(2, 4, 128, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    g = _gen(0)
+    q, k, v = (torch.randn(2, 4, 128, 64, device=DEV, dtype=torch.bfloat16, generator=g) for _ in range(3))
     out = custom_flash_attn.forward(q, k, v)
     ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True)
     torch.testing.assert_close(out.float(), ref, rtol=1e-2, atol=1e-2)
@@ -222,7 +229,8 @@ def test_matches_reference_test_vs_sdpa_fp32():
 def test_outputs_fully_written_and_guards_untouched():
     """NaN-poisoned outputs inside guard canaries: every element written, nothing outside."""
     B, H, N = 2, 3, 300
-    q, k, v = (torch.randn(B, H, N, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    g = _gen(11)
+    q, k, v = (torch.randn(B, H, N, 64, device=DEV, dtype=torch.bfloat16, generator=g) for _ in range(3))
     guard = 4096
     o_buf = torch.full((guard + B * H * N * 64 + guard,), float("nan"), device=DEV, dtype=torch.bfloat16)
     l_buf = torch.full((guard + B * H * N + guard,), float("nan"), device=DEV, dtype=torch.float32)
@@ -241,19 +249,22 @@ def test_outputs_fully_written_and_guards_untouched():
 
 
 def test_deterministic_bitwise():
-    q, k, v = (torch.randn(4, 8, 777, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    g = _gen(12)
+    q, k, v = (torch.randn(4, 8, 777, 64, device=DEV, dtype=torch.bfloat16, generator=g) for _ in range(3))
     o1, l1 = custom_flash_attn.forward_lse(q, k, v)
     o2, l2 = custom_flash_attn.forward_lse(q, k, v)
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
 
 
 def test_causality_bitwise():
-    q, k, v = (torch.randn(2, 4, 512, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    g = _gen(13)
+    q, k, v = (torch.randn(2, 4, 512, 64, device=DEV, dtype=torch.bfloat16, generator=g) for _ in range(3))
     o1 = custom_flash_attn.forward(q, k, v)
     i = 200
     k2, v2 = k.clone(), v.clone()
-    k2[:, :, i + 1:] = torch.randn_like(k2[:, :, i + 1:])
-    v2[:, :, i + 1:] = torch.randn_like(v2[:, :, i + 1:])
+    tail = k2[:, :, i + 1:].shape
+    k2[:, :, i + 1:] = torch.randn(tail, device=DEV, dtype=torch.bfloat16, generator=g)
+    v2[:, :, i + 1:] = torch.randn(tail, device=DEV, dtype=torch.bfloat16, generator=g)
     o2 = custom_flash_attn.forward(q, k2, v2)
     assert torch.equal(o1[:, :, : i + 1], o2[:, :, : i + 1])
     assert not torch.equal(o1[:, :, i + 1:], o2[:, :, i + 1:])
@@ -261,9 +272,10 @@ def test_causality_bitwise():
 
 def test_identical_keys_prefix_mean_and_constant_v():
     B, H, N = 1, 4, 300
-    q = torch.randn(B, H, N, 64, device=DEV, dtype=torch.bfloat16)
-    k = torch.randn(B, H, 1, 64, device=DEV, dtype=torch.bfloat16).expand(B, H, N, 64).contiguous()
-    v = torch.randn(B, H, N, 64, device=DEV, dtype=torch.bfloat16)
+    g = _gen(14)
+    q = torch.randn(B, H, N, 64, device=DEV, dtype=torch.bfloat16, generator=g)
+    k = torch.randn(B, H, 1, 64, device=DEV, dtype=torch.bfloat16, generator=g).expand(B, H, N, 64).contiguous()
+    v = torch.randn(B, H, N, 64, device=DEV, dtype=torch.bfloat16, generator=g)
     o, lse = custom_flash_attn.forward_lse(q, k, v)
     mean = torch.cumsum(v.double(), dim=2) / torch.arange(1, N + 1, device=DEV, dtype=torch.float64)[None, None, :, None]
     assert (o.double() - mean).abs().max().item() <= TOL_MAX
@@ -271,7 +283,8 @@ def test_identical_keys_prefix_mean_and_constant_v():
     ln = torch.log(torch.arange(1, N + 1, device=DEV, dtype=torch.float64))
     assert (lse.double() - (s + ln)).abs().max().item() <= TOL_LSE
     ones = torch.ones_like(v)
-    o1 = custom_flash_attn.forward(q * 3, torch.randn_like(q) * 3, ones)
+    k3 = torch.randn(q.shape, device=DEV, dtype=torch.bfloat16, generator=g)
+    o1 = custom_flash_attn.forward(q * 3, k3 * 3, ones)
     assert (o1.float() - 1).abs().max().item() <= 1e-2
 
 
@@ -283,18 +296,20 @@ def test_empty_inputs():
 
 
 def test_error_paths_on_device():
-    q = torch.randn(1, 2, 16, 64, device=DEV, dtype=torch.bfloat16)
+    g = _gen(15)
+    q = torch.randn(1, 2, 16, 64, device=DEV, dtype=torch.bfloat16, generator=g)
     with pytest.raises(RuntimeError, match="^K_mat must be contiguous$"):
         custom_flash_attn.forward(q, q.transpose(2, 3).contiguous().transpose(2, 3), q)
     with pytest.raises(RuntimeError, match="Use bfloat16"):
         custom_flash_attn.forward(q.half(), q.half(), q.half())
     with pytest.raises(RuntimeError, match="head_dim must be 64"):
-        x = torch.randn(1, 2, 16, 128, device=DEV, dtype=torch.bfloat16)
+        x = torch.randn(1, 2, 16, 128, device=DEV, dtype=torch.bfloat16, generator=g)
         custom_flash_attn.forward(x, x, x)
 
 
 def test_runs_on_side_stream():
-    q, k, v = (torch.randn(2, 4, 300, 64, device=DEV, dtype=torch.bfloat16) for _ in range(3))
+    g = _gen(16)
+    q, k, v = (torch.randn(2, 4, 300, 64, device=DEV, dtype=torch.bfloat16, generator=g) for _ in range(3))
     ref = custom_flash_attn.forward(q, k, v)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())

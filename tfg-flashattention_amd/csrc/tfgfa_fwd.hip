@@ -38,6 +38,12 @@
 //   Loads past the sequence end return zero (buffer range check): the zero-fill of partial
 //   tiles.
 //
+// Epilogue
+//   O is normalised, written to LDS (head dim 64: the wave's Q stage; head dim 128: a share of
+//   the ring after a final barrier) and read back so that each lane stores 16 B of one row:
+//   every store instruction writes whole 128-B (or 256-B) rows, non-temporally.  Storing the
+//   O^T accumulators directly wrote 16 B of each of 32 rows per instruction.
+//
 // MFMA chaining without an LDS round trip (v_mfma_f32_32x32x16_bf16, fp32 accumulate)
 //   S^T = K . Q^T  : A = K tile rows (32 keys x 16 d, ds_read_b128), B = Q^T (16 d x 32
 //                    queries, held in registers).  Accumulator lane l holds query l%32 and 16
@@ -750,6 +756,52 @@ __device__ __forceinline__ void steady_rest(WaveState<Sh>& w, const Lds& lds, in
   }
 }
 
+// The epilogue's O store for a wave's 32 rows.  The O^T accumulators give lane (r, h) head dims
+// 32i + 8g + 4h .. +3 of row r, so storing them directly writes 16 B of each of 32 rows per
+// store instruction.  Instead the normalised rows go through `stage` (32 rows of 2*kD bytes,
+// 16-B chunk c of row r at physical chunk c ^ (r % (kD/8)): the 8-B writes of consecutive rows
+// and the 16-B reads of one row hit distinct banks), and each lane then stores 16 B of one
+// row: kD/8 lanes write a whole row, one store instruction 8 (head dim 64) or 4 (head dim 128)
+// whole rows.  Whole-row stores are non-temporal (O is not read again here, and full lines need
+// no write combining in the L2).  With masked head dims (D < kD) rows are only partly written,
+// and those stores stay ordinary.  The stage is the wave's alone: LDS accesses of one wave
+// complete in order, so the reads see the writes without a barrier.
+template <class Sh>
+__device__ __forceinline__ void store_o(const WaveState<Sh>& w, unsigned char* stage, float inv_l,
+                                        int lane, typename Sh::T* ohead, long long row_stride,
+                                        int q0, int Nq, int d_chunks) {
+  typedef typename Sh::T T;
+  typedef typename Elem<T>::v4 v4;
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int kChunks = Sh::kD / 8;  // 16-B chunks per row
+  constexpr int kRowB = Sh::kD * 2;
+  const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 2 * Sh::kDH; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      // Register 4g + e of tile i holds dim 32i + 8g + 4h + e: chunk 4i + g, bytes 8h .. 8h+7.
+      v4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = (T)(w.o[i][4 * g + e] * inv_l);
+      const int c = 4 * i + g;
+      *reinterpret_cast<v4*>(stage + r * kRowB + ((c ^ (r % kChunks)) << 4) + 8 * h) = x;
+    }
+  constexpr int kRowsPerStore = 64 / kChunks;
+#pragma unroll
+  for (int t = 0; t < 32 / kRowsPerStore; ++t) {
+    const int R = kRowsPerStore * t + lane / kChunks, c = lane % kChunks;
+    const u32x4 val = *reinterpret_cast<const u32x4*>(stage + R * kRowB + ((c ^ (R % kChunks)) << 4));
+    if (q0 + R < Nq && (!Sh::kMaskD || c < d_chunks)) {
+      u32x4* dst = reinterpret_cast<u32x4*>(ohead + (long long)(q0 + R) * row_stride + 8 * c);
+      if constexpr (Sh::kMaskD)
+        *dst = val;
+      else
+        __builtin_nontemporal_store(val, dst);
+    }
+  }
+}
+
 // Element strides of one (B, H, N, D) operand: batch, head, row (the last dim is contiguous).
 struct Strides {
   long long b, h, n;
@@ -944,25 +996,21 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   int lane_e;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
   const int qrow_e = q0 + (lane_e & 31), h_e = lane_e >> 5;
-  if (qrow_e < Nq) {
-    const float inv_l = 1.0f / l_o;
-    T* orow = kDense ? O + dense_head + (long long)qrow_e * Sh::kD
-                     : O + bb * os.b + hh * os.h + (long long)qrow_e * os.n;
-#pragma unroll
-    for (int i = 0; i < 2 * Sh::kDH; ++i)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        // Register 4g + r of tile i holds dim 32i + 8g + 4h + r.
-        const int d0 = 32 * i + 8 * g + 4 * h_e;
-        v4 x;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] = (T)(w.o[i][4 * g + r] * inv_l);
-        if (!Sh::kMaskD || d0 < D) *reinterpret_cast<v4*>(orow + d0) = x;
-      }
-    if (Sh::kLse && LSE != nullptr && h_e == 0) {
-      LSE[(size_t)bh * Nq + qrow_e] = (w.m_run + __builtin_amdgcn_logf(l_all)) * kLn2;
-    }
+  // O leaves through LDS (store_o).  Head dim 64: the wave's own Q stage, unused since the
+  // prologue.  Head dim 128: a share of the K/V ring, free once every wave is past this barrier
+  // (every K/V read was consumed by an MFMA, every transfer waited for).
+  unsigned char* ostage;
+  if constexpr (Sh::kQStage) {
+    ostage = qstage;
+  } else {
+    lds_barrier();
+    ostage = ring + wave * (kWaveRows * Sh::kD * 2);
   }
+  T* ohead = kDense ? O + dense_head : O + bb * os.b + hh * os.h;
+  store_o<Sh>(w, ostage, 1.0f / l_o, lane_e, ohead, kDense ? (long long)Sh::kD : os.n, q0, Nq,
+              a.d_chunks);
+  if (Sh::kLse && LSE != nullptr && h_e == 0 && qrow_e < Nq)
+    LSE[(size_t)bh * Nq + qrow_e] = (w.m_run + __builtin_amdgcn_logf(l_all)) * kLn2;
 }
 
 // ---------------------------------------------------------------------------------------
