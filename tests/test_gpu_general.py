@@ -36,6 +36,26 @@ def _rand(shape, seed, dtype, sigma=1.0):
     return x.to(DEV), x.float().numpy()
 
 
+def _cu_count():
+    return custom_flash_attn.device_info()["cu_count"]
+
+
+def _heads(grid, B, nq):
+    """Heads per batch row that send a (B, H, nq) problem to one kernel: "split" (the split-key
+    kernel, whose grid is chosen while B * H * ceil(nq / 128) is at most the CU count) or
+    "regular" (fwd_kernel, one workgroup per 128-row query block)."""
+    nqb = (nq + 127) // 128
+    if grid == "split":
+        assert B * 3 * nqb <= _cu_count()
+        return 3
+    return _cu_count() // (B * nqb) + 1
+
+
+def _sample(x, B, H):
+    """Heads (0, 0), (0, 1) and (B-1, H-1) of a (B, H, ...) array: the oracle checks these."""
+    return np.stack([x[0, 0], x[0, 1], x[B - 1, H - 1]])[None]
+
+
 def _check(o, lse, o_ref, lse_ref, label):
     o = o.float().cpu().numpy().astype(np.float64)
     lse = lse.cpu().numpy().astype(np.float64)
@@ -46,35 +66,46 @@ def _check(o, lse, o_ref, lse_ref, label):
     assert d.max() <= TOL_MAX and d.mean() <= TOL_MEAN and dl.max() <= TOL_LSE, label
 
 
+@pytest.mark.parametrize("grid", ["split", "regular"])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("D", [8, 16, 32, 40, 64, 72, 96, 120, 128])
 @pytest.mark.parametrize("N,causal", [(65, True), (300, True), (300, False)])
-def test_dtypes_and_head_dims(dt, D, N, causal):
+def test_dtypes_and_head_dims(grid, dt, D, N, causal):
     dtype = DTYPES[dt]
-    q, qn = _rand((2, 3, N, D), 7 * D + N, dtype, 2.0)
-    k, kn = _rand((2, 3, N, D), 7 * D + N + 1, dtype, 2.0)
-    v, vn = _rand((2, 3, N, D), 7 * D + N + 2, dtype)
+    B = 2
+    H = _heads(grid, B, N)
+    q, qn = _rand((B, H, N, D), 7 * D + N, dtype, 2.0)
+    k, kn = _rand((B, H, N, D), 7 * D + N + 1, dtype, 2.0)
+    v, vn = _rand((B, H, N, D), 7 * D + N + 2, dtype)
     scale = 1.0 / math.sqrt(D)
     o, lse = custom_flash_attn.attention(q, k, v, causal=causal, return_lse=True)
     torch.cuda.synchronize()
     assert o.dtype == dtype
-    o_ref, l_ref = attention_c(qn, kn, vn, scale, causal)
-    _check(o, lse, o_ref, l_ref, f"{dt} D={D} N={N} causal={causal}")
+    o_ref, l_ref = attention_c(_sample(qn, B, H), _sample(kn, B, H), _sample(vn, B, H), scale, causal)
+    o_s = torch.stack([o[0, 0], o[0, 1], o[B - 1, H - 1]])[None]
+    l_s = torch.stack([lse[0, 0], lse[0, 1], lse[B - 1, H - 1]])[None]
+    _check(o_s, l_s, o_ref, l_ref, f"{grid} grid (H={H}) {dt} D={D} N={N} causal={causal}")
 
 
+@pytest.mark.parametrize("grid", ["split", "regular"])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("nq,nk", [(37, 300), (300, 37), (1, 129), (129, 1), (1000, 1500), (640, 64)])
 @pytest.mark.parametrize("causal", [True, False])
-def test_query_and_key_lengths_differ(dt, nq, nk, causal):
+def test_query_and_key_lengths_differ(grid, dt, nq, nk, causal):
     dtype = DTYPES[dt]
     D = 64 if nq % 2 else 128
-    q, qn = _rand((2, 2, nq, D), nq + 3 * nk, dtype, 2.0)
-    k, kn = _rand((2, 2, nk, D), nq + 3 * nk + 1, dtype, 2.0)
-    v, vn = _rand((2, 2, nk, D), nq + 3 * nk + 2, dtype)
+    B = 2
+    H = 2 if grid == "split" else _heads(grid, B, nq)
+    q, qn = _rand((B, H, nq, D), nq + 3 * nk, dtype, 2.0)
+    k, kn = _rand((B, H, nk, D), nq + 3 * nk + 1, dtype, 2.0)
+    v, vn = _rand((B, H, nk, D), nq + 3 * nk + 2, dtype)
     o, lse = custom_flash_attn.attention(q, k, v, causal=causal, return_lse=True)
     torch.cuda.synchronize()
-    o_ref, l_ref = attention_np(qn, kn, vn, 1.0 / math.sqrt(D), causal)
-    _check(o, lse, o_ref, l_ref, f"{dt} N_q={nq} N_k={nk} D={D} causal={causal}")
+    o_ref, l_ref = attention_np(_sample(qn, B, H), _sample(kn, B, H), _sample(vn, B, H),
+                                1.0 / math.sqrt(D), causal)
+    o_s = torch.stack([o[0, 0], o[0, 1], o[B - 1, H - 1]])[None]
+    l_s = torch.stack([lse[0, 0], lse[0, 1], lse[B - 1, H - 1]])[None]
+    _check(o_s, l_s, o_ref, l_ref, f"{grid} grid (H={H}) {dt} N_q={nq} N_k={nk} D={D} causal={causal}")
 
 
 @pytest.mark.parametrize("D", [96, 128])
@@ -138,27 +169,31 @@ def test_head_dim_128_at_gpt2_xl_length(dt):
     _check(o[:, :, rows], lse[:, :, rows], o_ref, l_ref, f"{dt} D=128 N=1024")
 
 
-def test_bf16_d64_general_path_equals_forward():
-    q, _ = _rand((2, 3, 257, 64), 41, torch.bfloat16, 3.0)
-    k, _ = _rand((2, 3, 257, 64), 42, torch.bfloat16, 3.0)
-    v, _ = _rand((2, 3, 257, 64), 43, torch.bfloat16)
+@pytest.mark.parametrize("grid", ["split", "regular"])
+def test_bf16_d64_general_path_equals_forward(grid):
+    H = _heads(grid, 2, 257)
+    q, _ = _rand((2, H, 257, 64), 41, torch.bfloat16, 3.0)
+    k, _ = _rand((2, H, 257, 64), 42, torch.bfloat16, 3.0)
+    v, _ = _rand((2, H, 257, 64), 43, torch.bfloat16)
     a = custom_flash_attn.attention(q, k, v)
     b = custom_flash_attn.forward(q, k, v)
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+@pytest.mark.parametrize("grid", ["split", "regular"])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("D", [64, 128, 40])
 @pytest.mark.parametrize("layout", ["contiguous", "projection views"])
 @pytest.mark.parametrize("nq,nk,causal", [(1024, 1024, True), (300, 520, False), (97, 97, True)])
-def test_o_only_call_equals_o_of_the_lse_call(dt, D, layout, nq, nk, causal):
+def test_o_only_call_equals_o_of_the_lse_call(grid, dt, D, layout, nq, nk, causal):
     """Without an LSE output the kernel does not keep the fp32 probability sum the LSE needs.
     O is normalised by the other sum (of the rounded probabilities) in both cases, so O is
     bitwise the same with and without the LSE, for every instance (dense GPT-2 layout,
     strided, head dims below the compiled ones)."""
     dtype = DTYPES[dt]
-    B, H = 2, 3
+    B = 2
+    H = _heads(grid, B, nq)
     if layout == "contiguous":
         q, qn = _rand((B, H, nq, D), 40 + D + nq, dtype, 3.0)
         k, kn = _rand((B, H, nk, D), 41 + D + nk, dtype, 3.0)
@@ -171,7 +206,10 @@ def test_o_only_call_equals_o_of_the_lse_call(dt, D, layout, nq, nk, causal):
     o_only = custom_flash_attn.attention(q, k, v, causal=causal)
     o, lse = custom_flash_attn.attention(q, k, v, causal=causal, return_lse=True)
     torch.cuda.synchronize()
-    assert torch.equal(o_only.view(torch.int16), o.view(torch.int16)), f"{dt} D={D} {layout}"
+    assert torch.equal(o_only.view(torch.int16), o.view(torch.int16)), f"{grid} {dt} D={D} {layout}"
     if layout == "contiguous" and nq == 97:
-        o_ref, l_ref = attention_c(qn, kn, vn, 1.0 / math.sqrt(D), causal)
-        _check(o_only, lse, o_ref, l_ref, f"O only, {dt} D={D}")
+        o_ref, l_ref = attention_c(_sample(qn, B, H), _sample(kn, B, H), _sample(vn, B, H),
+                                   1.0 / math.sqrt(D), causal)
+        o_s = torch.stack([o_only[0, 0], o_only[0, 1], o_only[B - 1, H - 1]])[None]
+        l_s = torch.stack([lse[0, 0], lse[0, 1], lse[B - 1, H - 1]])[None]
+        _check(o_s, l_s, o_ref, l_ref, f"O only, {grid} grid, {dt} D={D}")

@@ -57,7 +57,7 @@ def _oracle_check(o, lse, q, k, v, scale, causal, label):
     assert d.max() <= TOL_MAX and d.mean() <= TOL_MEAN and dl.max() <= TOL_LSE, label
 
 
-@pytest.mark.parametrize("B,H,N", [(2, 4, 256), (1, 3, 1000), (3, 2, 65), (2, 2, 1)])
+@pytest.mark.parametrize("B,H,N", [(2, 4, 256), (1, 3, 1000), (3, 2, 65), (2, 2, 1), (2, 25, 1024)])
 def test_gpt2_projection_views(B, H, N):
     """Q, K, V as (B, N, H, 64) projections viewed (B, H, N, 64); O written into a
     (B, N, H, 64) buffer through its transposed view."""
@@ -72,14 +72,16 @@ def test_gpt2_projection_views(B, H, N):
     assert out.data_ptr() == buf.data_ptr()
     o_ref, lse_ref = _contiguous_ref(q, k, v)
     _assert_same(out, lse, o_ref, lse_ref, "gpt2 views")
-    if N >= 65:
+    if N >= 65 and B * H <= 12:  # the B2 H25 N1024 case (the 128-row kernel) is checked bitwise only
         _oracle_check(out, lse, q, k, v, 0.125, True, f"gpt2 views B={B} H={H} N={N} vs oracle")
 
 
-def test_fused_qkv_buffer_and_padded_output():
+@pytest.mark.parametrize("H", [3, 129])
+def test_fused_qkv_buffer_and_padded_output(H):
     """Q, K, V interleaved in one (B, N, 3, H, 64) buffer (row stride 3*H*64), O into a
-    buffer with padded rows and heads; the padding keeps its sentinel."""
-    B, H, N, D = 2, 3, 300, 64
+    buffer with padded rows and heads; the padding keeps its sentinel.  H = 3 runs the split-key
+    kernel, H = 129 (774 query blocks) the 128-row one."""
+    B, N, D = 2, 300, 64
     _say(f"fused qkv B={B} H={H} N={N}")
     qkv = _randn((B, N, 3, H, D), seed=5, sigma=3.0)
     qkv[:, :, 2].div_(3.0)  # V ~ N(0, 1)
@@ -92,7 +94,8 @@ def test_fused_qkv_buffer_and_padded_output():
     _assert_same(out, lse, o_ref, lse_ref, "fused qkv")
     assert (big[:, :H, :, D:] == SENTINEL).all(), "row padding written"
     assert (big[:, H:] == SENTINEL).all(), "head padding written"
-    _oracle_check(out, lse, q, k, v, 0.125, True, "fused qkv vs oracle")
+    if H <= 3:
+        _oracle_check(out, lse, q, k, v, 0.125, True, "fused qkv vs oracle")
 
 
 @pytest.mark.parametrize("causal", [True, False])

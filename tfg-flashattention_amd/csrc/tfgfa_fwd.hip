@@ -351,6 +351,13 @@ __device__ __forceinline__ void issue_q_stage(i32x4 qdesc, int row_bytes, unsign
 // explicit vmcnt waits before each barrier.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// Workgroup barrier after this wave's own LDS writes (ds_write) and reads: s_barrier does not
+// wait for the wave's outstanding LDS operations, so they are waited for first; after it,
+// every wave sees the writes of every other.
+__device__ __forceinline__ void lds_write_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -380,8 +387,9 @@ struct WaveState {
   int voff[2][2];        // V^T transposing-read LDS offsets (within a V dim half, keys 0..15)
 };
 
-// S^T = K Q^T for key half kHalf of the tile in K slot kSlot (4 MFMAs per dim half).
-template <class Sh, int kSlot, int kHalf>
+// S^T = K Q^T for key half kHalf of the tile in K slot kSlot (4 MFMAs per dim half; dim half dh
+// at byte dh * kDhBytes of the slot).
+template <class Sh, int kSlot, int kHalf, int kDhBytes = kHalfTileBytes>
 __device__ __forceinline__ f32x16 qk_half(const WaveState<Sh>& w, const Lds& lds) {
   typedef typename Elem<typename Sh::T>::v8 v8;
   f32x16 acc;
@@ -389,7 +397,7 @@ __device__ __forceinline__ f32x16 qk_half(const WaveState<Sh>& w, const Lds& lds
   for (int t = 0; t < 16; ++t) acc[t] = 0.f;
 #pragma unroll
   for (int dh = 0; dh < Sh::kDH; ++dh) {
-    const unsigned char* kt = lds.k[kSlot] + dh * kHalfTileBytes + kHalf * 32 * kKRowBytes;
+    const unsigned char* kt = lds.k[kSlot] + dh * kDhBytes + kHalf * 32 * kKRowBytes;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const v8 a = *reinterpret_cast<const v8*>(kt + w.koff[c]);
@@ -401,13 +409,13 @@ __device__ __forceinline__ f32x16 qk_half(const WaveState<Sh>& w, const Lds& lds
 
 // O^T += V^T P^T for key half kHalf of the tile in V slot kSlot, with P^T = w.pb (4 MFMAs per
 // dim half).  Element e of chunk cc in lane half h is key 16*cc + 8*(e/4) + 4*h + e%4 of the
-// key half: two transposing reads of 4 keys each.
-template <class Sh, int kSlot, int kHalf>
+// key half: two transposing reads of 4 keys each.  Dim half dh at byte dh * kDhBytes of the slot.
+template <class Sh, int kSlot, int kHalf, int kDhBytes = kHalfTileBytes>
 __device__ __forceinline__ void pv_half(WaveState<Sh>& w, const Lds& lds) {
   typedef typename Elem<typename Sh::T>::v8 v8;
 #pragma unroll
   for (int dh = 0; dh < Sh::kDH; ++dh) {
-    const unsigned char* vt = lds.v[kSlot] + dh * kHalfTileBytes + kHalf * 32 * kKRowBytes;
+    const unsigned char* vt = lds.v[kSlot] + dh * kDhBytes + kHalf * 32 * kKRowBytes;
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
 #pragma unroll
@@ -1014,6 +1022,277 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
+// Small grids: split-key workgroups (fwd_split_kernel).
+//
+// When B * H * ceil(N_q / 128) workgroups of fwd_kernel leave most CUs idle, a launch takes as
+// long as its longest wave's chain of half-steps (4qb + 4 for query block qb), not its work.
+// Then each workgroup takes one 32-row query block, and its 4 waves split the block's 32-key
+// halves (wave w: halves w, w + 4, w + 8, ...): every wave runs its own online softmax over the
+// same 32 rows, with its own 2-slot ring of K and V halves in LDS, so no wave waits for another
+// until the merge.  The merge goes through LDS with the log-sum-exp rule over the 4 partial
+// states (offset m_w, rounded-probability sum lp_w, fp32 sum l_w, unnormalised O_w):
+//   M = max_w m_w,  a_w = 2^(m_w - M),  O = sum_w a_w O_w / sum_w a_w lp_w,
+//   LSE = (M + log2 sum_w a_w l_w) ln 2.
+// A wave with no half contributes m_w = -inf (a_w = 0).  The half-step is the tail path of
+// fwd_kernel (qk_half, mask_half, move_offset, exp_half, pv_half), unpipelined: at this size
+// the time is latency, and each wave has at most ceil(nH / 4) halves.
+constexpr int kHalfBytes = 32 * kKRowBytes;  // one 32-key half of K or V, one dim half: 4 KiB
+
+template <class Sh>
+struct SplitLayout {
+  // Waves per workgroup.  8 at head dim 64 (one half per wave at N = 256) measured no faster
+  // at B1 H12 N256 and slower from N = 1024 on.
+  static constexpr int kWaves = 4;
+  static constexpr int kSlotBytes = 2 * Sh::kDH * kHalfBytes;  // a K half, then a V half
+  static constexpr int kWaveBytes = 2 * kSlotBytes;             // the wave's 2-slot ring
+  static constexpr int kRingBytes = kWaves * kWaveBytes;
+  static constexpr int kQBytes = kWaveRows * Sh::kD * 2;        // the block's 32 Q rows
+  static constexpr int kOPartBytes = kWaveRows * Sh::kD * 4;    // one wave's O partial, fp32
+  static_assert(kWaves * kOPartBytes <= kRingBytes, "the O partials fit in the rings");
+  static constexpr int kLoadsPerHalf = 8 * Sh::kDH;             // 1-KiB transfers, K and V
+  static constexpr int kRowsPerWave = kWaveRows / kWaves;       // rows each wave merges
+};
+
+// Rows r0 .. r0 + 7 of one 32-row half (dim half dh) from the buffer at `desc` (rows row_bytes
+// apart) into LDS at dst + 128 * r0: lane i fills physical chunk i % 8 of row r0 + i / 8 with
+// the logical chunk the swizzle maps there (K swizzle for K and Q, V swizzle for V).
+template <class Sh, bool kVSwz>
+__device__ __forceinline__ void issue_rows8(i32x4 desc, int row_bytes, unsigned char* dst, int r0,
+                                            int dh, int lane, int d_chunks) {
+  const int row = r0 + (lane >> 3);
+  const int lc = 8 * dh + ((lane & 7) ^ (kVSwz ? swz_v(row) : swz_k(row)));
+  int off = row * row_bytes + (lc << 4);
+  if (Sh::kMaskD) off = lc < d_chunks ? off : kOutOfRange;
+  lds_transfer(desc, lds_addr(dst + r0 * kKRowBytes), off);
+}
+
+// Half u of K and V (32 rows each, every dim half) into ring slot `slot` of this wave.
+template <class Sh>
+__device__ __forceinline__ void issue_split_half(const StepArgs& a, unsigned char* slot, int u) {
+  const i32x4 kd = tile_desc(a.k_rsrc, 32 * u, a.k_row_bytes);
+  const i32x4 vd = tile_desc(a.v_rsrc, 32 * u, a.v_row_bytes);
+  unsigned char* vslot = slot + Sh::kDH * kHalfBytes;
+#pragma unroll
+  for (int dh = 0; dh < Sh::kDH; ++dh)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      issue_rows8<Sh, false>(kd, a.k_row_bytes, slot + dh * kHalfBytes, 8 * t, dh, a.lane, a.d_chunks);
+      issue_rows8<Sh, true>(vd, a.v_row_bytes, vslot + dh * kHalfBytes, 8 * t, dh, a.lane, a.d_chunks);
+    }
+}
+
+// One half u from ring slot kSlot: S, mask (diagonal or last partial half), offset check, P and
+// its sums, O += V P.
+template <class Sh, int kSlot>
+__device__ __forceinline__ void split_half(WaveState<Sh>& w, const Lds& lds, int u, const StepArgs& a) {
+  w.s = qk_half<Sh, kSlot, 0, kHalfBytes>(w, lds);
+  if (u >= a.nFull) mask_half(w, a.last_key - u * 32 - 4 * a.h);
+  move_offset(w, lane_max(w), a.scale_log2, a.inv_scale_log2);
+  exp_half(w, a.scale_log2);
+  pv_half<Sh, kSlot, 0, kHalfBytes>(w, lds);
+}
+
+template <class Sh>
+__global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_kernel(
+    const void* __restrict__ Qv, const void* __restrict__ Kv, const void* __restrict__ Vv,
+    void* __restrict__ Ov, float* __restrict__ LSE, int H, int BH, int Nq, int Nk, int D,
+    int nRB, float scale_log2, int causal, Strides qs, Strides ks, Strides vs, Strides os) {
+  typedef typename Sh::T T;
+  typedef typename Elem<T>::v8 v8;
+  typedef SplitLayout<Sh> L;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[L::kRingBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char qst[L::kQBytes];
+  __shared__ float stats[L::kWaves][3][kWaveRows];  // m, lp, l per wave and row
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r32 = lane & 31;
+  const int h = lane >> 5;
+  // Heaviest (last) query blocks first.
+  const int bid = blockIdx.x;
+  const int rb = nRB - 1 - bid / BH;
+  const int bh = bid % BH;
+  const int bb = bh / H, hh = bh - bb * H;
+  const T* Q = static_cast<const T*>(Qv) + bb * qs.b + hh * qs.h;
+  const T* K = static_cast<const T*>(Kv) + bb * ks.b + hh * ks.h;
+  const T* V = static_cast<const T*>(Vv) + bb * vs.b + hh * vs.h;
+  const int q_row_bytes = (int)qs.n * 2;
+  const int q0 = rb * kWaveRows;
+  const int qrow = q0 + r32;
+
+  StepArgs a;
+  a.k_row_bytes = (int)ks.n * 2;
+  a.v_row_bytes = (int)vs.n * 2;
+  a.k_rsrc = head_desc(K, Nk, a.k_row_bytes);
+  a.v_rsrc = head_desc(V, Nk, a.v_row_bytes);
+  a.d_chunks = D >> 3;
+  // Halves of the block: those starting at or below its last row (causal, top-left aligned) and
+  // below Nk; unmasked: wholly below its first row (causal) and wholly below Nk.
+  const int kv_end = causal ? min(Nk, q0 + kWaveRows) : Nk;
+  const int nH = (kv_end + 31) / 32;
+  a.nFull = causal ? min(q0 / 32, Nk / 32) : Nk / 32;
+  a.nAct = wave < nH ? (nH - 1 - wave) / L::kWaves + 1 : 0;  // this wave's halves
+  a.nT = 0;
+  a.wave = wave;
+  a.lane = lane;
+  a.h = h;
+  a.last_key = causal ? min(qrow, Nk - 1) : Nk - 1;
+  a.scale_log2 = scale_log2;
+  a.inv_scale_log2 = 1.0f / scale_log2;
+
+  unsigned char* wring = ring + wave * L::kWaveBytes;
+  const Lds lds = {{wring, wring + L::kSlotBytes, nullptr},
+                   {wring + Sh::kDH * kHalfBytes, wring + L::kSlotBytes + Sh::kDH * kHalfBytes}};
+
+  // This wave's quarter of the Q block (rows 8w .. 8w + 7 of each dim half), then its first two
+  // halves.  Rows past N_q read zero.
+  if (wave < kWaveRows / 8) {
+    const i32x4 qd = tile_desc(head_desc(Q, Nq, q_row_bytes), q0, q_row_bytes);
+#pragma unroll
+    for (int dh = 0; dh < Sh::kDH; ++dh)
+      issue_rows8<Sh, false>(qd, q_row_bytes, qst + dh * kHalfBytes, 8 * wave, dh, lane, a.d_chunks);
+  }
+  if (a.nAct > 0) issue_split_half<Sh>(a, wring, wave);
+  if (a.nAct > 1) issue_split_half<Sh>(a, wring + L::kSlotBytes, wave + L::kWaves);
+
+  WaveState<Sh> w;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) w.koff[c] = r32 * kKRowBytes + (((2 * c + h) ^ swz_k(r32)) << 4);
+  {
+    const int g = lane >> 4, jj = lane & 15;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int sr = 0; sr < 2; ++sr) {
+        const int row = 8 * sr + 4 * (g >> 1) + (jj >> 2);
+        const int d0 = 32 * dt + 16 * (g & 1) + 4 * (jj & 3);
+        w.voff[dt][sr] = row * kKRowBytes + (((d0 >> 3) ^ swz_v(row)) << 4) + (d0 & 7) * 2;
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 2 * Sh::kDH; ++i)
+#pragma unroll
+    for (int t = 0; t < 16; ++t) w.o[i][t] = 0.f;
+  w.m_run = -INFINITY;
+  w.thr = -INFINITY;
+  w.l_run = 0.f;
+  w.l_p = 0.f;
+
+  // Q has landed once only the half transfers (issued after it) may be in flight; the barrier
+  // makes every wave's quarter visible.
+  if (a.nAct > 1)
+    wait_vmcnt<2 * L::kLoadsPerHalf>();
+  else if (a.nAct == 1)
+    wait_vmcnt<L::kLoadsPerHalf>();
+  else
+    wait_vmcnt<0>();
+  lds_barrier();
+#pragma unroll
+  for (int dh = 0; dh < Sh::kDH; ++dh)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      w.qop[4 * dh + c] = *reinterpret_cast<const v8*>(qst + dh * kHalfBytes + r32 * kKRowBytes +
+                                                        (((2 * c + h) ^ swz_k(r32)) << 4));
+
+  for (int i = 0; i < a.nAct; ++i) {
+    const int u = wave + L::kWaves * i;
+    if (i + 1 < a.nAct)
+      wait_vmcnt<L::kLoadsPerHalf>();
+    else
+      wait_vmcnt<0>();
+    if (i & 1)
+      split_half<Sh, 1>(w, lds, u, a);
+    else
+      split_half<Sh, 0>(w, lds, u, a);
+    if (i + 2 < a.nAct) {
+      // The slot's LDS reads are complete before the transfers into it are issued.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      issue_split_half<Sh>(a, wring + (i & 1) * L::kSlotBytes, u + 2 * L::kWaves);
+    }
+  }
+
+  // Merge.  Each wave publishes its row statistics and its unnormalised O rows (fp32, row-major,
+  // 16-B chunk c of row r at physical chunk c ^ (r % (kD/4))) over the rings, which every wave
+  // has finished with once it is past the first barrier (all transfers waited for, every K/V
+  // read consumed).
+  const float lp = pair_sum(w.l_p);
+  const float lr = Sh::kLse ? pair_sum(w.l_run) : 0.f;
+  int lane_e;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
+  const int r_e = lane_e & 31, h_e = lane_e >> 5;
+  constexpr int kC4 = Sh::kD / 4;   // 16-B fp32 chunks per O row
+  constexpr int kRowB = Sh::kD * 4;
+  lds_write_barrier();
+  unsigned char* opart = ring + wave * L::kOPartBytes;
+#pragma unroll
+  for (int i = 0; i < 2 * Sh::kDH; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      // Register 4g + e of tile i holds dim 32i + 8g + 4h + e: fp32 chunk 8i + 2g + h.
+      const f32x4 x = {w.o[i][4 * g], w.o[i][4 * g + 1], w.o[i][4 * g + 2], w.o[i][4 * g + 3]};
+      const int c = 8 * i + 2 * g + h_e;
+      *reinterpret_cast<f32x4*>(opart + r_e * kRowB + ((c ^ (r_e % kC4)) << 4)) = x;
+    }
+  if (h_e == 0) {
+    stats[wave][0][r_e] = w.m_run;
+    stats[wave][1][r_e] = lp;
+    stats[wave][2][r_e] = lr;
+  }
+  lds_write_barrier();
+  // Wave w combines rows w * kRowsPerWave .. +kRowsPerWave - 1: item -> (row, 8 head dims),
+  // kD/8 items per row, so each lane stores 16 B and kD/8 lanes a whole row (non-temporal, as
+  // in store_o).
+  constexpr int kC8 = Sh::kD / 8;
+  constexpr int kItems = L::kRowsPerWave * kC8;
+  T* O = static_cast<T*>(Ov) + bb * os.b + hh * os.h;
+#pragma unroll
+  for (int pass = 0; pass < (kItems + 63) / 64; ++pass) {
+    const int item = 64 * pass + lane_e;
+    if (kItems % 64 != 0 && item >= kItems) break;
+    const int R = L::kRowsPerWave * wave + item / kC8, c8 = item % kC8;
+    float M = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < L::kWaves; ++v) M = fmaxf(M, stats[v][0][R]);
+    float lsum = 0.f, lrun = 0.f;
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < L::kWaves; ++v) {
+      const float av = __builtin_amdgcn_exp2f(stats[v][0][R] - M);
+      lsum = fmaf(av, stats[v][1][R], lsum);
+      if constexpr (Sh::kLse) lrun = fmaf(av, stats[v][2][R], lrun);
+      const unsigned char* src = ring + v * L::kOPartBytes + R * kRowB;
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(src + (((2 * c8) ^ (R % kC4)) << 4));
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + (((2 * c8 + 1) ^ (R % kC4)) << 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc0[e] = fmaf(av, x0[e], acc0[e]);
+        acc1[e] = fmaf(av, x1[e], acc1[e]);
+      }
+    }
+    const float inv = 1.0f / lsum;
+    typename Elem<T>::v8 ov;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ov[e] = (T)(acc0[e] * inv);
+      ov[4 + e] = (T)(acc1[e] * inv);
+    }
+    const int qr = q0 + R;
+    if (qr < Nq && (!Sh::kMaskD || c8 < a.d_chunks)) {
+      u32x4* dst = reinterpret_cast<u32x4*>(O + (long long)qr * os.n + 8 * c8);
+      if constexpr (Sh::kMaskD)
+        *dst = __builtin_bit_cast(u32x4, ov);
+      else
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, ov), dst);
+    }
+    if (Sh::kLse && LSE != nullptr && c8 == 0 && qr < Nq)
+      LSE[(size_t)bh * Nq + qr] = (M + __builtin_amdgcn_logf(lrun)) * kLn2;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Host side: argument validation, cached device properties, launch.
 
 struct DeviceInfo {
@@ -1109,6 +1388,14 @@ static int validate(const void* q, const void* k, const void* v, const void* o, 
   return TFGFA_OK;
 }
 
+// fwd_kernel's grid of 128-row query blocks is at most one workgroup per CU: the split-key
+// kernel runs the launch instead (a 4x larger grid, a longest wave chain about 4x shorter).
+// Measured crossover (bf16, head dims 64 and 128): faster at every grid up to the CU count
+// (B1 H12 N256 6.66 -> 5.07 us, B1 H16 N1024 15.9 -> 10.1 us, B1 H16 N2048 27.9 -> 24.6 us),
+// slower from twice that (B2 H32 N1024 17.5 -> 27.9 us).  The choice depends on the sizes only,
+// never on strides or outputs, so every instance of one problem takes the same arithmetic.
+static bool use_split_grid(long long blocks, int cu_count) { return blocks <= cu_count; }
+
 struct LaunchArgs {
   const void *q, *k, *v;
   void* o;
@@ -1126,8 +1413,25 @@ static void launch_instance(const LaunchArgs& a, hipStream_t stream) {
                      a.causal, a.qs, a.ks, a.vs, a.os);
 }
 
+template <class Sh>
+static void launch_split_instance(const LaunchArgs& a, hipStream_t stream) {
+  const int nRB = (a.Nq + kWaveRows - 1) / kWaveRows;
+  hipLaunchKernelGGL((fwd_split_kernel<Sh>), dim3(a.BH * nRB), dim3(SplitLayout<Sh>::kWaves * 64), 0, stream, a.q,
+                     a.k, a.v, a.o, a.lse, a.H, a.BH, a.Nq, a.Nk, a.D, nRB, a.scale_log2,
+                     a.causal, a.qs, a.ks, a.vs, a.os);
+}
+
 template <int kD, typename T>
-static void launch_dims(const LaunchArgs& a, bool dense, hipStream_t stream) {
+static void launch_dims(const LaunchArgs& a, bool dense, bool split, hipStream_t stream) {
+  if (split) {
+    if (a.D != kD)
+      launch_split_instance<Shape<kD, T, true>>(a, stream);
+    else if (a.lse != nullptr)
+      launch_split_instance<Shape<kD, T, false>>(a, stream);
+    else
+      launch_split_instance<Shape<kD, T, false, false>>(a, stream);
+    return;
+  }
   if (a.D != kD) {
     launch_instance<Shape<kD, T, true>, false>(a, stream);
     return;
@@ -1177,17 +1481,21 @@ static int launch(const void* q, const void* k, const void* v, void* o, float* l
     return x.b == y.b && x.h == y.h && x.n == y.n;
   };
   const bool dense = Nq == Nk && same(a.qs, dq) && same(a.ks, dq) && same(a.vs, dq) && same(a.os, dq);
+  int cu_count = 0;
+  const int ist = tfgfa_device_info(&cu_count, nullptr, nullptr, 0);
+  if (ist != TFGFA_OK) return ist;
+  const bool split = use_split_grid((long long)a.BH * a.nQB, cu_count);
   const hipStream_t stream = (hipStream_t)hip_stream;
   if (dtype == TFGFA_DTYPE_BF16) {
     if (D <= 64)
-      launch_dims<64, __bf16>(a, dense, stream);
+      launch_dims<64, __bf16>(a, dense, split, stream);
     else
-      launch_dims<128, __bf16>(a, dense, stream);
+      launch_dims<128, __bf16>(a, dense, split, stream);
   } else {
     if (D <= 64)
-      launch_dims<64, _Float16>(a, dense, stream);
+      launch_dims<64, _Float16>(a, dense, split, stream);
     else
-      launch_dims<128, _Float16>(a, dense, stream);
+      launch_dims<128, _Float16>(a, dense, split, stream);
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? TFGFA_OK : -(int)e;
