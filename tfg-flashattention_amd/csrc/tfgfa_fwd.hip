@@ -1035,7 +1035,9 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
 //   LSE = (M + log2 sum_w a_w l_w) ln 2.
 // A wave with no half contributes m_w = -inf (a_w = 0).  The half-step is the tail path of
 // fwd_kernel (qk_half, mask_half, move_offset, exp_half, pv_half), unpipelined: at this size
-// the time is latency, and each wave has at most ceil(nH / 4) halves.
+// the time is latency, and each wave has at most ceil(nH / 4) halves.  A wave with exactly two
+// (both loaded by the prologue) computes them together (split_pair): at B1 H12 N256 that took
+// the launch from 5.06 to 4.19 us.
 constexpr int kHalfBytes = 32 * kKRowBytes;  // one 32-key half of K or V, one dim half: 4 KiB
 
 template <class Sh>
@@ -1090,6 +1092,28 @@ __device__ __forceinline__ void split_half(WaveState<Sh>& w, const Lds& lds, int
   move_offset(w, lane_max(w), a.scale_log2, a.inv_scale_log2);
   exp_half(w, a.scale_log2);
   pv_half<Sh, kSlot, 0, kHalfBytes>(w, lds);
+}
+
+// Halves u0 (ring slot 0) and u1 (slot 1) together: two independent S chains, one offset check
+// over both (every P of both halves is then within the margin), then P and O += V P for each.
+// For a wave with exactly two halves, the common case of the latency-bound grids this kernel
+// runs, this is a shorter dependency chain than two split_half calls.
+template <class Sh>
+__device__ __forceinline__ void split_pair(WaveState<Sh>& w, const Lds& lds, int u0, int u1,
+                                           const StepArgs& a) {
+  const f32x16 s0 = qk_half<Sh, 0, 0, kHalfBytes>(w, lds);
+  w.s = qk_half<Sh, 1, 0, kHalfBytes>(w, lds);
+  if (u1 >= a.nFull) mask_half(w, a.last_key - u1 * 32 - 4 * a.h);
+  const float mx1 = lane_max(w);
+  const f32x16 s1 = w.s;
+  w.s = s0;
+  if (u0 >= a.nFull) mask_half(w, a.last_key - u0 * 32 - 4 * a.h);
+  move_offset(w, fmaxf(lane_max(w), mx1), a.scale_log2, a.inv_scale_log2);
+  exp_half(w, a.scale_log2);
+  pv_half<Sh, 0, 0, kHalfBytes>(w, lds);
+  w.s = s1;
+  exp_half(w, a.scale_log2);
+  pv_half<Sh, 1, 0, kHalfBytes>(w, lds);
 }
 
 template <class Sh>
@@ -1197,6 +1221,11 @@ __global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_ker
       w.qop[4 * dh + c] = *reinterpret_cast<const v8*>(qst + dh * kHalfBytes + r32 * kKRowBytes +
                                                         (((2 * c + h) ^ swz_k(r32)) << 4));
 
+  if (a.nAct == 2) {
+    // Both halves were issued by the prologue.
+    wait_vmcnt<0>();
+    split_pair<Sh>(w, lds, wave, wave + L::kWaves, a);
+  } else {
   for (int i = 0; i < a.nAct; ++i) {
     const int u = wave + L::kWaves * i;
     if (i + 1 < a.nAct)
@@ -1213,11 +1242,12 @@ __global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_ker
       issue_split_half<Sh>(a, wring + (i & 1) * L::kSlotBytes, u + 2 * L::kWaves);
     }
   }
+  }
 
   // Merge.  Each wave publishes its row statistics and its unnormalised O rows (fp32, row-major,
-  // 16-B chunk c of row r at physical chunk c ^ (r % (kD/4))) over the rings, which every wave
-  // has finished with once it is past the first barrier (all transfers waited for, every K/V
-  // read consumed).
+  // 16-B chunk c of row r at physical chunk c ^ (r % (kD/4))) over its own ring, which only it
+  // used: its transfers were all waited for, and its LDS accesses complete in order, so its K/V
+  // reads come before these writes.  One barrier then publishes every wave's rows.
   const float lp = pair_sum(w.l_p);
   const float lr = Sh::kLse ? pair_sum(w.l_run) : 0.f;
   int lane_e;
@@ -1225,8 +1255,8 @@ __global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_ker
   const int r_e = lane_e & 31, h_e = lane_e >> 5;
   constexpr int kC4 = Sh::kD / 4;   // 16-B fp32 chunks per O row
   constexpr int kRowB = Sh::kD * 4;
-  lds_write_barrier();
-  unsigned char* opart = ring + wave * L::kOPartBytes;
+  static_assert(L::kOPartBytes <= L::kWaveBytes, "a wave's O partial fits in its ring");
+  unsigned char* opart = wring;
 #pragma unroll
   for (int i = 0; i < 2 * Sh::kDH; ++i)
 #pragma unroll
@@ -1263,7 +1293,7 @@ __global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_ker
       const float av = __builtin_amdgcn_exp2f(stats[v][0][R] - M);
       lsum = fmaf(av, stats[v][1][R], lsum);
       if constexpr (Sh::kLse) lrun = fmaf(av, stats[v][2][R], lrun);
-      const unsigned char* src = ring + v * L::kOPartBytes + R * kRowB;
+      const unsigned char* src = ring + v * L::kWaveBytes + R * kRowB;
       const f32x4 x0 = *reinterpret_cast<const f32x4*>(src + (((2 * c8) ^ (R % kC4)) << 4));
       const f32x4 x1 = *reinterpret_cast<const f32x4*>(src + (((2 * c8 + 1) ^ (R % kC4)) << 4));
 #pragma unroll
