@@ -17,10 +17,12 @@ Prints one JSON line.  ``value`` is TFLOP/s with the FlashAttention causal conve
 reference's PyTorch CPU attention path (the "manual" branch of src/py/model_inference.py:68-75)
 on this host's cores.  ``configs`` times every BASELINE.json attention config (1-4, plus the
 drop-in O-only call at config 3) by per-launch events: the median of at least 200 launches
-after a warm-up of at least 0.1 s, whatever --steps and --warmup say.
+after a warm-up of at least 0.1 s, whatever --steps and --warmup say.  ``triton_wrapper_surface``
+times the general entry point the same way on fp16 and head dim 128 (the surface of the
+reference's Triton wrapper, src/py/triton_implementation.py:184-197).
 
 Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 2000] [--no-cpu-baseline] [--no-strided]
-                      [--no-decode] [--no-generate] [--no-configs]
+                      [--no-decode] [--no-generate] [--no-configs] [--no-surface]
        python bench.py --profile WORKLOAD [--launches 15]   (a bounded run for rocprofv3 --pmc)
        python bench.py --calibrate-copy MIB                 (copy kernels of known bytes)
 """
@@ -564,8 +566,70 @@ def time_configs(dev):
     return out
 
 
-PROFILE_WORKLOADS = ("config1", "config2", "config3", "config3_o_only", "config4", "decode",
-                     "decode_split_B1_H25_L1024", "decode_split_B1_H16_L8192")
+# The Triton wrapper's surface (src/py/triton_implementation.py:184-197): fp16, head dims up to
+# 128, an explicit scale.  (name, B, H, N, D, dtype, sigma_qk, seed); causal, scale 1/sqrt(D).
+SURFACE_LEGS = (("fp16_config3_shape", 8, 25, 1024, 64, "f16", 3.0, 2001),
+                ("bf16_d128_B8_H16_N1024", 8, 16, 1024, 128, "bf16", 1.0, 2002),
+                ("bf16_d128_B1_H16_N8192", 1, 16, 8192, 128, "bf16", 1.0, 2003))
+
+
+def time_surface(dev):
+    """The general entry point (tfgfa_fwd through custom_flash_attn.attention's _C.fwd_general)
+    on the Triton wrapper's surface: fp16 at the config-3 shape and bf16 head dim 128 at two
+    shapes, O + LSE, causal.  Timed as the configs legs: input sets rotated, >= 0.1 s of warm-up,
+    the median of 200 per-launch event timings."""
+    import torch
+
+    from custom_flash_attn import _C
+
+    dtypes = {"bf16": (torch.bfloat16, 0), "f16": (torch.float16, 1)}
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    out = {}
+    for name, b, h, n, d, dt, sigma, seed in SURFACE_LEGS:
+        tdt, code = dtypes[dt]
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        per_set = 4 * b * h * n * d * 2
+        nsets = max(2, min(6, -(-400_000_000 // per_set)))
+        sets = []
+        for _ in range(nsets):
+            q, k, v = ((torch.randn(b, h, n, d, device=dev, generator=gen) * sg).to(tdt)
+                       for sg in (sigma, sigma, 1.0))
+            o = torch.empty_like(q)
+            lse = torch.empty(b, h, n, device=dev, dtype=torch.float32)
+            sets.append((q, k, v, o, lse))
+        scale = 1.0 / math.sqrt(d)
+
+        def step(i, sets=sets, b=b, h=h, n=n, d=d, code=code, scale=scale):
+            q, k, v, o, lse = sets[i % len(sets)]
+            _C.fwd_general(q.data_ptr(), q.stride(), k.data_ptr(), k.stride(), v.data_ptr(),
+                           v.stride(), o.data_ptr(), o.stride(), lse.data_ptr(), b, h, n, n, d,
+                           code, scale, True, sh)
+
+        _warm(step)
+        med, mean = _per_call_ms(step, stream)
+        flops = 4.0 * b * h * n * n * d / 2.0
+        byts = 2.0 * 4 * b * h * n * d + 4.0 * b * h * n
+        tf = flops / (med * 1e-3) / 1e12
+        out[name] = {
+            "shape": f"B{b} H{h} N{n} d{d}", "dtype": dt, "outputs": "O + LSE",
+            "ms_per_call_median": round(med, 5), "ms_per_call_mean": round(mean, 5),
+            "calls": MIN_PER_CALL, "input_sets_rotated": nsets, "value": round(tf, 2),
+            "unit": "TFLOP/s",
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                         "hbm_ceiling_frac_of_mfma_peak": round(
+                             min(1.0, flops / byts * PEAK_HBM_GBS * 1e9 / (PEAK_BF16_TFLOPS * 1e12)), 4)},
+        }
+        del sets
+    torch.cuda.empty_cache()
+    out["entry"] = "custom_flash_attn._C.fwd_general -> tfgfa_fwd (fp16 dense peak = bf16's, 2.5 PFLOP/s)"
+    return out
+
+
+PROFILE_WORKLOADS = ("config1", "config2", "config3", "config3_o_only", "config4", "strided_gpt2_views",
+                     "fp16_config3_shape", "bf16_d128_B8_H16_N1024", "bf16_d128_B1_H16_N8192",
+                     "decode", "decode_split_B1_H25_L1024", "decode_split_B1_H16_L8192")
 
 
 def profile_workload(dev, name, launches):
@@ -594,6 +658,37 @@ def profile_workload(dev, name, launches):
             _C.fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                    lse.data_ptr() if with_lse else 0, cfg.B, cfg.H, cfg.N, cfg.D, cfg.scale, True, sh)
         shape = f"B{cfg.B} H{cfg.H} N{cfg.N} d{cfg.D}, {'O + LSE' if with_lse else 'O'}"
+    elif name == "strided_gpt2_views":
+        gen.manual_seed(2003)
+        sets = []
+        for _ in range(N_SETS):
+            q, k, v = ((torch.randn(B, N, H, D, device=dev, generator=gen) * sg).to(torch.bfloat16)
+                       .transpose(1, 2) for sg in (SIGMA_QK, SIGMA_QK, SIGMA_V))
+            sets.append((q, k, v, torch.empty(B, N, H, D, device=dev, dtype=torch.bfloat16).transpose(1, 2),
+                         torch.empty(B, H, N, device=dev, dtype=torch.float32)))
+
+        def step(i):
+            q, k, v, o, lse = sets[i % N_SETS]
+            _C.fwd_strided(q.data_ptr(), q.stride(), k.data_ptr(), k.stride(), v.data_ptr(), v.stride(),
+                           o.data_ptr(), o.stride(), lse.data_ptr(), B, H, N, D, SCALE, True, sh)
+        shape = f"B{B} H{H} N{N} d{D} as (B, N, H, 64) projection views, O + LSE"
+    elif name in [leg[0] for leg in SURFACE_LEGS]:
+        _, b, h, n, d, dt, sigma, seed = next(leg for leg in SURFACE_LEGS if leg[0] == name)
+        tdt, code = (torch.bfloat16, 0) if dt == "bf16" else (torch.float16, 1)
+        gen.manual_seed(seed)
+        nsets = max(2, min(6, -(-400_000_000 // (4 * b * h * n * d * 2))))
+        sets = []
+        for _ in range(nsets):
+            q, k, v = ((torch.randn(b, h, n, d, device=dev, generator=gen) * sg).to(tdt)
+                       for sg in (sigma, sigma, 1.0))
+            sets.append((q, k, v, torch.empty_like(q), torch.empty(b, h, n, device=dev, dtype=torch.float32)))
+
+        def step(i, b=b, h=h, n=n, d=d, code=code):
+            q, k, v, o, lse = sets[i % len(sets)]
+            _C.fwd_general(q.data_ptr(), q.stride(), k.data_ptr(), k.stride(), v.data_ptr(),
+                           v.stride(), o.data_ptr(), o.stride(), lse.data_ptr(), b, h, n, n, d,
+                           code, 1.0 / math.sqrt(d), True, sh)
+        shape = f"B{b} H{h} N{n} d{d} {dt}, O + LSE"
     else:
         if name == "decode":
             b, h, n, append = B, H, N, True
@@ -646,6 +741,8 @@ def main():
                     help="skip the token-generation leg (the reference's generate() benchmark)")
     ap.add_argument("--no-strided", action="store_true",
                     help="skip the second timing of the same workload on strided (B, N, H, 64) views")
+    ap.add_argument("--no-surface", action="store_true",
+                    help="skip the fp16 / head dim 128 legs (the Triton wrapper's surface)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config legs (BASELINE.json configs 1-4, per-launch medians)")
     ap.add_argument("--cpu-heads", type=int, default=200,
@@ -810,6 +907,8 @@ def main():
         "value": round(flops_per_fwd() / (ms_py * 1e-3) / 1e12, 2), "unit": "TFLOP/s"}
     if not args.no_configs:
         result["configs"] = time_configs(dev)
+    if not args.no_surface:
+        result["triton_wrapper_surface"] = time_surface(dev)
     if not args.no_strided:
         result["strided_gpt2_views"] = time_strided_views(dev)
     if not args.no_decode:

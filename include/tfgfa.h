@@ -67,7 +67,8 @@ extern "C" {
 #define TFGFA_ERR_STRIDE         8  /* strides outside what the entry point takes         */
 #define TFGFA_ERR_CACHE          9  /* k_new/v_new given without cache_seqlens            */
 #define TFGFA_ERR_DTYPE         10  /* dtype is not a TFGFA_DTYPE_* value                 */
-#define TFGFA_ERR_SCRATCH       11  /* tfgfa_decode_noalloc: partials exceed its scratch    */
+#define TFGFA_ERR_SCRATCH       11  /* reserved: tfgfa_decode_noalloc limits its split to
+                                       its scratch and no longer returns it                */
 
 /* Element types of q, k, v, o (fp32 accumulation and softmax either way). */
 #define TFGFA_DTYPE_BF16 0
@@ -230,15 +231,33 @@ int tfgfa_decode(const void* q, const int64_t* q_strides,
 size_t tfgfa_decode_workspace_size(int B, int H, int N_max, int D);
 
 /*
+ * The split tfgfa_decode chooses: the number of workgroups S each head's cache is divided
+ * over (1: one workgroup per head, no workspace used) on a device of cu_count CUs with a
+ * workspace of workspace_bytes (0: none).  A workspace of exactly
+ *   (B*H*128 rounded up to 256) + B*H*S*(D+1)*4 bytes
+ * runs the same split.  0 when a size is out of range.  Host arithmetic only (no HIP call).
+ * No counterpart in the reference: for callers sizing a workspace exactly.
+ */
+int tfgfa_decode_splits(int B, int H, int N_max, int D, int cu_count, size_t workspace_bytes);
+
+/*
+ * Bytes of tfgfa_decode_noalloc's static scratch (320 KiB).  No counterpart in the reference.
+ */
+size_t tfgfa_decode_scratch_bytes(void);
+
+/*
  * tfgfa_decode without a workspace argument, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  Operands, results and errors as tfgfa_decode; the arrival
  * words and split partials go to a static 320 KiB scratch array of the library instead (one
- * per GPU, held until the process ends), and the call allocates nothing.  Results are
- * bitwise those of tfgfa_decode with a workspace of tfgfa_decode_workspace_size bytes.
- * Limit: the split the library chooses must fit the scratch, arrival words plus
- * B*H*S*(D+1)*4 bytes <= 320 KiB, which holds on a 256-CU MI355X for every shape (at most
- * 280 KiB); otherwise TFGFA_ERR_SCRATCH before any launch.  Every call on one GPU shares that
+ * per GPU, held until the process ends), and the call allocates nothing.  The scratch acts
+ * as a 320 KiB workspace: results are bitwise those of tfgfa_decode with a workspace of
+ * tfgfa_decode_scratch_bytes() bytes, and so with any workspace that holds the library's
+ * split (arrival words plus B*H*S*(D+1)*4 bytes), which 320 KiB does on a 256-CU MI355X
+ * for every shape (at most 280 KiB).  On a part where the split would not fit, the call
+ * splits only as far as the scratch holds (correct, a different split).  The first call on
+ * a device looks the scratch up (hipGetSymbolAddress), also when that call is made during
+ * stream capture.  Every call on one GPU shares that
  * GPU's scratch (it keeps the last call's partials, and its arrival words end at zero):
  * calls that overlap on one GPU, e.g. on two streams at once, race and must be ordered by
  * the caller.

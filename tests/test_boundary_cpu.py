@@ -60,12 +60,59 @@ def lib():
 def test_library_exports_every_declared_symbol(lib):
     names = _header_functions()
     assert names == ["tfgfa_abi_version", "tfgfa_decode", "tfgfa_decode_bf16",
-                     "tfgfa_decode_noalloc", "tfgfa_decode_workspace_bytes",
-                     "tfgfa_decode_workspace_size",
+                     "tfgfa_decode_noalloc", "tfgfa_decode_scratch_bytes", "tfgfa_decode_splits",
+                     "tfgfa_decode_workspace_bytes", "tfgfa_decode_workspace_size",
                      "tfgfa_device_info", "tfgfa_fwd", "tfgfa_fwd_bf16", "tfgfa_fwd_bf16_strided",
                      "tfgfa_strerror"]
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/tfgfa.h but not exported"
+
+
+def _split_bytes(bh, D, S):
+    """Workspace bytes of a split of S (include/tfgfa.h, tfgfa_decode_splits): arrival words
+    (B*H*128 rounded up to 256), then B*H*S partials of D + 1 floats; none for S = 1."""
+    return 0 if S <= 1 else -(-bh * 128 // 256) * 256 + bh * S * (D + 1) * 4
+
+
+def test_decode_noalloc_scratch_holds_the_split_on_256_cus(lib):
+    """tfgfa_decode_noalloc uses its static scratch as a workspace: on a 256-CU MI355X the split
+    it then chooses is the full-workspace split for every shape (so its results are bitwise
+    tfgfa_decode's), at most 280 KiB; with more CUs it splits only as far as the scratch holds."""
+    lib.tfgfa_decode_splits.restype = ctypes.c_int
+    lib.tfgfa_decode_splits.argtypes = [ctypes.c_int] * 5 + [ctypes.c_size_t]
+    lib.tfgfa_decode_scratch_bytes.restype = ctypes.c_size_t
+    lib.tfgfa_decode_workspace_size.restype = ctypes.c_size_t
+    lib.tfgfa_decode_workspace_size.argtypes = [ctypes.c_int] * 4
+    scratch = lib.tfgfa_decode_scratch_bytes()
+    assert scratch == 320 * 1024
+    worst = 0
+    lengths = (1, 512, 1023, 1024, 1025, 2048, 4096, 8192, 16384, 32768, 1 << 20)
+    for bh in list(range(1, 131)) + [200, 1000]:
+        for D in range(8, 129, 8):
+            for n in lengths:
+                full = lib.tfgfa_decode_workspace_size(1, bh, n, D)
+                S = lib.tfgfa_decode_splits(1, bh, n, D, 256, full)
+                assert S >= 1 and (S == 1 or 2 * bh <= 256)
+                assert lib.tfgfa_decode_splits(1, bh, n, D, 256, scratch) == S, (bh, D, n)
+                worst = max(worst, _split_bytes(bh, D, S))
+    assert worst <= 280 * 1024, worst
+    # A part with more CUs: the full-workspace split may outgrow the scratch; the scratch's own
+    # split always fits it.
+    outgrown = 0
+    for cu in (304, 512, 1024):
+        for bh in (1, 8, 64, cu // 2):
+            for D in (64, 128):
+                full = lib.tfgfa_decode_workspace_size(1, bh, 1 << 16, D)
+                s_full = lib.tfgfa_decode_splits(1, bh, 1 << 16, D, cu, full)
+                s_scr = lib.tfgfa_decode_splits(1, bh, 1 << 16, D, cu, scratch)
+                assert 1 <= s_scr <= s_full and _split_bytes(bh, D, s_scr) <= scratch
+                outgrown += s_scr < s_full
+    assert outgrown > 0
+    # Out-of-range sizes.
+    assert lib.tfgfa_decode_splits(0, 1, 16, 64, 256, 0) == 0
+    assert lib.tfgfa_decode_splits(1, 1, 16, 36, 256, 0) == 0
+    assert lib.tfgfa_decode_splits(1, 1, 16, 64, 0, 0) == 0
+    assert lib.tfgfa_decode_splits(1, 4, 8192, 64, 256, 0) == 1  # no workspace: no split
 
 
 def test_abi_version(lib):
@@ -540,8 +587,8 @@ def test_decode_workspace_not_cached_under_graph_capture(monkeypatch):
     a = cfa._decode_workspace(dev, 256)
     b = cfa._decode_workspace(dev, 256)
     assert a.numel() >= 256 and b.numel() >= 256
-    assert a.data_ptr() != b.data_ptr() or a is not b
-    assert cfa._WORKSPACES == {}
+    assert a is not b  # a fresh buffer per captured call
+    assert cfa._WORKSPACES == {}  # and none of them cached
 
     class _S:
         cuda_stream = 1234
@@ -551,4 +598,5 @@ def test_decode_workspace_not_cached_under_graph_capture(monkeypatch):
     c = cfa._decode_workspace(dev, 256)
     d = cfa._decode_workspace(dev, 128)
     assert c is d and c.numel() >= 256
+    assert c is not a and c is not b  # eager calls never get a captured call's buffer
     assert list(cfa._WORKSPACES) == [(dev, 1234)]

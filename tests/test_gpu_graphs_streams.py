@@ -207,3 +207,29 @@ def test_two_streams_at_once():
     for a, b in zip(outs1, outs2):
         assert _same(a, ref1)
         assert torch.equal(b, ref2)
+
+
+def test_decode_captured_without_workspace_replays():
+    """decode() captured with no workspace argument takes a fresh buffer from the capture's
+    memory pool, released after the call; a later allocation in the same graph (here a
+    temporary that a kernel fills with 1.0) may reuse that memory, so each replay's decode
+    starts on arrival words that hold whatever the previous replay left there.  Every replay,
+    with eager decode() calls on the same stream in between, is bitwise the eager result."""
+    B, H, N, D = 1, 4, 4096, 64  # split heads (B*H far below the CU count)
+    q = _randn((B, H, D), 1, 2.0)
+    kc, vc = _randn((B, H, N, D), 2, 2.0), _randn((B, H, N, D), 3)
+    lens = torch.full((B,), N, dtype=torch.int32, device=DEV)
+    ref = custom_flash_attn.decode(q, kc, vc, lens, return_lse=True)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        o, lse = custom_flash_attn.decode(q, kc, vc, lens, return_lse=True)
+        tmp = torch.empty(1 << 20, device=DEV, dtype=torch.float32)
+        tmp.fill_(1.0)
+    for rep in range(5):
+        g.replay()
+        eager_o, eager_l = custom_flash_attn.decode(q, kc, vc, lens, return_lse=True)
+        torch.cuda.synchronize()
+        assert _same(o, ref[0]) and torch.equal(lse, ref[1]), f"replay {rep}"
+        assert _same(eager_o, ref[0]) and torch.equal(eager_l, ref[1]), f"eager after replay {rep}"
+    _say("decode captured without a workspace: 5 replays bitwise equal to eager")

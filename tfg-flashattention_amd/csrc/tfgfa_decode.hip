@@ -798,6 +798,13 @@ static int device_scratch(void** out) {
 
 // Bytes of one partial set (every head, one split) for head dim D: o_s[D] and lse_s.
 static size_t split_bytes(long long bh, int D) { return (size_t)bh * (size_t)(D + 1) * sizeof(float); }
+
+// Splits a workspace of `bytes` (arrival words `ab` bytes, then partial sets of `per_split`)
+// holds; at least 1 (one split needs no workspace).
+static int workspace_splits(size_t bytes, size_t ab, size_t per_split) {
+  if (bytes <= ab) return 1;
+  return (int)std::max((size_t)1, std::min((size_t)INT32_MAX, (bytes - ab) / per_split));
+}
 // Bytes of the arrival words at the start of a workspace: one per head, kArriveStride apart.
 static size_t arrive_bytes(long long bh) { return ((size_t)bh * kArriveStride + 255) / 256 * 256; }
 
@@ -865,21 +872,16 @@ static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
   if (st != TFGFA_OK) return st;
   const size_t per_split = split_bytes(bh, D);
   const size_t ab = arrive_bytes(bh);
-  int S, C;
   if (use_scratch) {
-    // The split the library would choose with an unbounded workspace must fit the scratch:
-    // then the result is bitwise that of tfgfa_decode with a full workspace.
-    choose_split((int)bh, N_max, D, cu, kMaxSplits, &S, &C);
-    if (S > 1 && ab + (size_t)S * per_split > kScratchBytes) return TFGFA_ERR_SCRATCH;
+    // The scratch is the workspace: the split is limited to what it holds, exactly as for a
+    // caller's workspace of that size.
     const int sst = device_scratch(&workspace);
     if (sst != TFGFA_OK) return sst;
     workspace_bytes = kScratchBytes;
-  } else {
-    const int ws_splits = workspace && workspace_bytes > ab
-                              ? (int)std::min((size_t)INT32_MAX, (workspace_bytes - ab) / per_split)
-                              : 0;
-    choose_split((int)bh, N_max, D, cu, std::max(1, ws_splits), &S, &C);
   }
+  int S, C;
+  choose_split((int)bh, N_max, D, cu,
+               workspace_splits(workspace ? workspace_bytes : 0, ab, per_split), &S, &C);
   if (bh * S > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
 
   const hipStream_t stream = (hipStream_t)hip_stream;
@@ -931,6 +933,20 @@ extern "C" size_t tfgfa_decode_workspace_size(int B, int H, int N_max, int D) {
   const size_t blocks = ((size_t)N_max + kWorkspaceRows - 1) / kWorkspaceRows;
   return arrive_bytes((long long)B * H) + split_bytes((long long)B * H, D) * blocks;
 }
+
+extern "C" int tfgfa_decode_splits(int B, int H, int N_max, int D, int cu_count,
+                                   size_t workspace_bytes) {
+  using namespace tfgfa_dec;
+  if (B <= 0 || H <= 0 || N_max <= 0 || D < 8 || D > kMaxD || (D & 7) || cu_count <= 0) return 0;
+  const long long bh = (long long)B * H;
+  if (bh > INT32_MAX) return 0;
+  int S, C;
+  choose_split((int)bh, N_max, D, cu_count,
+               workspace_splits(workspace_bytes, arrive_bytes(bh), split_bytes(bh, D)), &S, &C);
+  return S;
+}
+
+extern "C" size_t tfgfa_decode_scratch_bytes(void) { return tfgfa_dec::kScratchBytes; }
 
 extern "C" size_t tfgfa_decode_workspace_bytes(int B, int H, int N_max) {
   return tfgfa_decode_workspace_size(B, H, N_max, tfgfa_dec::kD);

@@ -1575,8 +1575,7 @@ extern "C" const char* tfgfa_strerror(int status) {
     case TFGFA_ERR_ALIGNMENT: return "misaligned pointer (q/k/v/o need 16 B, lse 4 B)";
     case TFGFA_ERR_CACHE: return "k_new/v_new (cache append) need cache_seqlens";
     case TFGFA_ERR_SCRATCH:
-      return "the decode split needs more partials than the library's static scratch holds "
-             "(320 KiB); call tfgfa_decode with a workspace";
+      return "reserved status (decode scratch): not returned by this library";
     case TFGFA_ERR_STRIDE:
       return "unsupported strides (last dim 1; b, h, n non-negative multiples of 8; n >= head dim; "
              "o without overlapping elements)";
