@@ -438,12 +438,70 @@ def time_decode(dev, steps=2000):
 SPLIT_SHAPES = ((1, 25, 1024), (1, 16, 8192))  # (B, H, cache rows): one GPT-2-XL sequence, a long one
 
 
+def _read_floor(dev, rows, reps, per_graph):
+    """What a graph-replayed step of `rows` cache rows (K and V, 64 bf16 each) cannot beat:
+    an empty kernel (a one-element fill) and a plain streaming read of the same bytes
+    (tfgfa_stream_read: 16-B loads, one word written per workgroup), each replayed from a HIP
+    graph of per_graph launches like the step, the buffers rotating through more than the
+    Infinity Cache."""
+    import torch
+
+    from custom_flash_attn import _C
+
+    stream = torch.cuda.current_stream(dev)
+    one = torch.zeros(1, device=dev)
+    nbytes = rows * 128
+    nsets = max(2, -(-600_000_000 // nbytes))
+    bufs = [torch.empty(nbytes, device=dev, dtype=torch.uint8).random_(0, 255) for _ in range(nsets)]
+    sink = torch.empty(4096, device=dev, dtype=torch.int32)
+    res = {}
+
+    def read(i):
+        _C.stream_read(bufs[i % nsets].data_ptr(), nbytes, sink.data_ptr(),
+                       torch.cuda.current_stream(dev).cuda_stream)
+
+    for name, fn in (("empty_kernel", lambda i: one.fill_(float(i & 1))), ("plain_read", read)):
+        for i in range(2 * nsets):
+            fn(i)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for i in range(per_graph):
+                    fn(i)
+        stream.wait_stream(side)
+        _warm(lambda i: graph.replay(), min_calls=3)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        res[f"{name}_ms"] = round(start.elapsed_time(end) / (reps * per_graph), 5)
+        del graph
+    res["plain_read_bytes"] = nbytes
+    res["plain_read_GBps"] = round(nbytes / (res["plain_read_ms"] * 1e-3) / 1e9, 1)
+    del bufs
+    return res
+
+
+def _read_floor_or_note(dev, rows, reps, per_graph):
+    try:
+        return _read_floor(dev, rows, reps, per_graph)
+    except RuntimeError as e:  # e.g. a library call that cannot be captured in a graph here
+        return {"unavailable": str(e)[:200]}
+
+
 def time_decode_split(dev, reps=20):
     """Decode steps whose B*H leaves most CUs idle, so each head's cache is split over several
-    workgroups and a second kernel merges the partials: one GPT-2-XL sequence (B=1, H=25, a
-    1024-row cache) and a long context (B=1, H=16, 8192 rows).  bf16, d=64, every row valid, no
-    append; caches rotate through more than the Infinity Cache; steps replayed from a HIP graph
-    (no host gaps between the two launches of a step)."""
+    workgroups and the last one of a head to finish merges the partials: one GPT-2-XL sequence
+    (B=1, H=25, a 1024-row cache) and a long context (B=1, H=16, 8192 rows).  bf16, d=64, every
+    row valid, no append; caches rotate through more than the Infinity Cache; steps replayed from
+    a HIP graph.  The same graph is then timed with every cache length 1: the step's fixed cost
+    (launch, split, exchange of the partials), against which the bytes-dependent part reads."""
     import torch
 
     from custom_flash_attn import _C
@@ -481,25 +539,32 @@ def time_decode_split(dev, reps=20):
                 for i in range(per_graph):
                     step(i, torch.cuda.current_stream(dev).cuda_stream)
         stream.wait_stream(side)
-        _warm(lambda i: graph.replay(), min_calls=3)
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-        ms = start.elapsed_time(end) / (reps * per_graph)
+
+        def timed_replays():
+            _warm(lambda i: graph.replay(), min_calls=3)
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            end.record(stream)
+            torch.cuda.synchronize()
+            return start.elapsed_time(end) / (reps * per_graph)
+
+        ms = timed_replays()
         algo = b * h * (2 * n * D * 2 + D * 2 + D * 2 + 4)
         gbs = algo / (ms * 1e-3) / 1e9
         out[f"B{b}_H{h}_L{n}"] = {
             "ms_per_step_graph": round(ms, 5), "steps": reps * per_graph,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": algo},
+            "floor": _read_floor_or_note(dev, b * h * n * 2, reps, per_graph),
         }
         del sets, graph
-    out["workload"] = ("decode step split over workgroups + merge kernel, bf16 d=64, all rows valid, "
-                       "caches rotating through HBM, HIP-graph replay")
+    out["workload"] = ("decode step split over workgroups (the last-arriving workgroup of a head "
+                       "merges its partials), bf16 d=64, all rows valid, caches rotating through "
+                       "HBM, HIP-graph replay; floor: the same replay of an empty kernel and of a "
+                       "plain streaming read (tfgfa_stream_read) of the step's K and V bytes")
     return out
 
 

@@ -273,6 +273,14 @@ int tfgfa_decode_noalloc(const void* q, const int64_t* q_strides,
                          void* hip_stream);
 
 /*
+ * A plain streaming read of `bytes` bytes at device pointer p (16-byte aligned, a multiple of
+ * 16 bytes), writing meaningless words into `sink` (4096 uint32, device memory): the floor a
+ * decode step's cache reads are measured against (bench.py's decode_split legs).  No counterpart
+ * in the reference; measurement only.
+ */
+int tfgfa_stream_read(const void* p, size_t bytes, void* sink, void* hip_stream);
+
+/*
  * Human-readable text for a status code returned by any tfgfa_* function.
  * The string is static.  Replaces the TORCH_CHECK messages of
  * src/cpp/torch_bind.cpp:13-19, :41 for errors detected below the binding

@@ -63,7 +63,7 @@ def test_library_exports_every_declared_symbol(lib):
                      "tfgfa_decode_noalloc", "tfgfa_decode_scratch_bytes", "tfgfa_decode_splits",
                      "tfgfa_decode_workspace_bytes", "tfgfa_decode_workspace_size",
                      "tfgfa_device_info", "tfgfa_fwd", "tfgfa_fwd_bf16", "tfgfa_fwd_bf16_strided",
-                     "tfgfa_strerror"]
+                     "tfgfa_stream_read", "tfgfa_strerror"]
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/tfgfa.h but not exported"
 

@@ -192,3 +192,30 @@ def test_errors_come_back_as_status_codes(lib):
     st = lib.tfgfa_decode_bf16(q.data_ptr(), z3, q.data_ptr(), z4, q.data_ptr(), z4, None, None, None, None,
                                None, q.data_ptr(), z3, None, 1, 1, 4, 128, 0.125, None, 0, _stream())
     assert st > 0 and b"head dimension" in lib.tfgfa_strerror(st)
+
+
+@pytest.mark.parametrize("nbytes", [1 << 20, 6553600, 33554432 + 48])
+def test_stream_read_reads_every_word(lib, nbytes):
+    """tfgfa_stream_read (the decode legs' plain-read floor): workgroup w folds 16-B words
+    [w * per_wg, (w + 1) * per_wg) with xor into sink[w]; checked against the same fold on the
+    CPU, so every byte of the buffer was read."""
+    lib.tfgfa_stream_read.restype = ctypes.c_int
+    lib.tfgfa_stream_read.argtypes = [P, ctypes.c_size_t, P, P]
+    g = torch.Generator(device=DEV).manual_seed(nbytes & 0xFFFF)
+    buf = torch.randint(-2**31, 2**31 - 1, (nbytes // 4,), device=DEV, dtype=torch.int32, generator=g)
+    sink = torch.zeros(4096, device=DEV, dtype=torch.int32)
+    _ok(lib, lib.tfgfa_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(), _stream()))
+    torch.cuda.synchronize()
+    n16 = nbytes // 16
+    wg = max(256, min(4096, n16 // 2048))
+    per = -(-n16 // wg)
+    words = buf.cpu().numpy().view(np.uint32).reshape(n16, 4)
+    words = np.bitwise_xor.reduce(words, axis=1)
+    exp = np.zeros(wg, dtype=np.uint32)
+    for w in range(wg):
+        chunk = words[w * per:(w + 1) * per]
+        exp[w] = np.bitwise_xor.reduce(chunk) if chunk.size else 0
+    got = sink.cpu().numpy().view(np.uint32)[:wg]
+    assert np.array_equal(got, exp)
+    _say(f"stream_read {nbytes} B: {wg} workgroups, every word folded")
+    assert lib.tfgfa_stream_read(buf.data_ptr() + 4, 16, sink.data_ptr(), _stream()) != 0  # misaligned

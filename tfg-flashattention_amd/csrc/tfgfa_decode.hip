@@ -923,7 +923,53 @@ static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
   return TFGFA_OK;
 }
 
+// A plain streaming read: the floor a decode step's cache reads are measured against.  Workgroup
+// w reads 16-B words [w * per_wg, (w + 1) * per_wg) of the buffer (kReadUnroll loads in flight
+// per thread), folds them with xor and writes one word to sink[w % kSinkWords], so that no load
+// can be dropped; the sink's contents mean nothing.
+constexpr int kReadUnroll = 8;
+constexpr int kSinkWords = 4096;
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, long long n16,
+                                                          int per_wg, uint32_t* __restrict__ sink) {
+  const long long base = (long long)blockIdx.x * per_wg;
+  uint32_t acc = 0;
+  for (int i0 = 0; i0 < per_wg; i0 += 256 * kReadUnroll) {
+    u32x4 v[kReadUnroll];
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u) {
+      const int i = i0 + u * 256 + (int)threadIdx.x;
+      const long long j = base + i;
+      v[u] = (i < per_wg && j < n16) ? p[j] : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < kReadUnroll; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, o);
+  __shared__ uint32_t wave_acc[4];
+  if ((threadIdx.x & 63) == 0) wave_acc[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    sink[blockIdx.x % kSinkWords] = wave_acc[0] ^ wave_acc[1] ^ wave_acc[2] ^ wave_acc[3];
+}
+
 }  // namespace tfgfa_dec
+
+extern "C" int tfgfa_stream_read(const void* p, size_t bytes, void* sink, void* hip_stream) {
+  using namespace tfgfa_dec;
+  if (bytes == 0) return TFGFA_OK;
+  if (p == nullptr || sink == nullptr) return TFGFA_ERR_NULL_POINTER;
+  if ((((uintptr_t)p) & 15u) || (bytes & 15u) || (((uintptr_t)sink) & 3u)) return TFGFA_ERR_ALIGNMENT;
+  const long long n16 = (long long)(bytes / 16);
+  // At least 256 workgroups (every CU streams), each reading at least 32 KiB, at most 4096.
+  const long long wg = std::max(256LL, std::min(4096LL, n16 / 2048));
+  const long long per_wg = (n16 + wg - 1) / wg;
+  if (per_wg > INT32_MAX) return TFGFA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)wg), dim3(256), 0, (hipStream_t)hip_stream,
+                     static_cast<const u32x4*>(p), n16, (int)per_wg, static_cast<uint32_t*>(sink));
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TFGFA_OK : -(int)e;
+}
 
 extern "C" size_t tfgfa_decode_workspace_size(int B, int H, int N_max, int D) {
   using namespace tfgfa_dec;

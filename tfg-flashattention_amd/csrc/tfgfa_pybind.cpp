@@ -175,6 +175,13 @@ PYBIND11_MODULE(_C, m) {
         py::arg("o_strides"), py::arg("lse"), py::arg("B"), py::arg("H"), py::arg("N_max"),
         py::arg("D"), py::arg("dtype"), py::arg("softmax_scale"), py::arg("workspace"),
         py::arg("workspace_bytes"), py::arg("stream"));
+  m.def("stream_read", [](std::uintptr_t p, std::size_t bytes, std::uintptr_t sink, std::uintptr_t stream) {
+    const int st = tfgfa_stream_read(reinterpret_cast<const void*>(p), bytes,
+                                     reinterpret_cast<void*>(sink), reinterpret_cast<void*>(stream));
+    if (st != TFGFA_OK)
+      throw std::runtime_error(std::string("tfgfa_stream_read failed: ") + tfgfa_strerror(st));
+  }, "A plain streaming read of `bytes` device bytes (a measurement floor)", py::arg("p"),
+        py::arg("bytes"), py::arg("sink"), py::arg("stream"));
   m.def("decode_workspace_bytes", [](int B, int H, int N_max) {
     return tfgfa_decode_workspace_bytes(B, H, N_max);
   });
