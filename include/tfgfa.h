@@ -53,7 +53,10 @@
 extern "C" {
 #endif
 
-#define TFGFA_ABI_VERSION 7
+/* 8: tfgfa_decode_splits, tfgfa_decode_scratch_bytes and tfgfa_stream_read added;
+ * tfgfa_decode_noalloc splits only as far as its scratch holds instead of returning
+ * TFGFA_ERR_SCRATCH. */
+#define TFGFA_ABI_VERSION 8
 
 /* Status codes (> 0: invalid argument). */
 #define TFGFA_OK                 0
