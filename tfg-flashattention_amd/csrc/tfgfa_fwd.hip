@@ -818,11 +818,18 @@ struct Strides {
 // One instance per (head dims, element type, dim masking, layout).  kDense: every operand is
 // the contiguous (B, H, N, kD) layout with N_q = N_k, so row strides are compile-time and the
 // stride arguments are not read.
+//
+// Argument order: the device pass preloads the first 14 argument dwords into SGPRs at wave
+// launch (-amdgpu-kernarg-preload-count; s[0:1] hold the argument segment's address).
+// Everything a dense workgroup needs before its first loads (Q, K, V, the sizes, the causal
+// flag) and O and the scale sit there, so it issues its loads without a scalar load from the
+// argument segment first (an L2 round trip on a CU's first workgroup: 0.3 us of a config-1
+// launch).  The LSE pointer, H, D and the strides follow; the strided instances load them.
 template <class Sh, bool kDense>
 __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
     const void* __restrict__ Qv, const void* __restrict__ Kv, const void* __restrict__ Vv,
-    void* __restrict__ Ov, float* __restrict__ LSE, int H, int BH, int Nq, int Nk, int D,
-    int nQB, float scale_log2, int causal, Strides qs, Strides ks, Strides vs, Strides os) {
+    void* __restrict__ Ov, int BH, int Nq, int Nk, int nQB, int causal, float scale_log2,
+    float* __restrict__ LSE, int H, int D, Strides qs, Strides ks, Strides vs, Strides os) {
   typedef typename Sh::T T;
   typedef typename Elem<T>::v8 v8;
   typedef typename Elem<T>::v4 v4;
@@ -918,6 +925,8 @@ __global__ __launch_bounds__(kThreads, Sh::kDH == 1 ? 3 : 2) void fwd_kernel(
   issue_tile<Sh>(a.k_rsrc, a.k_row_bytes, lds.k[0], 0, wave, a.k_lane);
   if (a.nT > 1) issue_tile<Sh>(a.k_rsrc, a.k_row_bytes, lds.k[1], kTileKeys, wave, a.k_lane);
   issue_tile<Sh>(a.v_rsrc, a.v_row_bytes, lds.v[0], 0, wave, a.v_lane);
+  // The LSE pointer is not among the preloaded arguments: load it while the tiles are in flight.
+  if constexpr (Sh::kLse) asm volatile("" ::"s"(LSE));
 
   // K A-operand, d chunk c: row r32 (+32 for the second key half, an immediate), logical 16-B
   // chunk 2c + h.
@@ -1116,11 +1125,14 @@ __device__ __forceinline__ void split_pair(WaveState<Sh>& w, const Lds& lds, int
   pv_half<Sh, 1, 0, kHalfBytes>(w, lds);
 }
 
-template <class Sh>
+// Arguments in fwd_kernel's order (the preloaded dwords first).  kDense as for fwd_kernel; the
+// dense instances are what makes a small contiguous launch start without a scalar load (B1 H12
+// N256: 4.10 -> 3.76 us).
+template <class Sh, bool kDense>
 __global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_kernel(
     const void* __restrict__ Qv, const void* __restrict__ Kv, const void* __restrict__ Vv,
-    void* __restrict__ Ov, float* __restrict__ LSE, int H, int BH, int Nq, int Nk, int D,
-    int nRB, float scale_log2, int causal, Strides qs, Strides ks, Strides vs, Strides os) {
+    void* __restrict__ Ov, int BH, int Nq, int Nk, int nRB, int causal, float scale_log2,
+    float* __restrict__ LSE, int H, int D, Strides qs, Strides ks, Strides vs, Strides os) {
   typedef typename Sh::T T;
   typedef typename Elem<T>::v8 v8;
   typedef SplitLayout<Sh> L;
@@ -1139,17 +1151,18 @@ __global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_ker
   const int bid = blockIdx.x;
   const int rb = nRB - 1 - bid / BH;
   const int bh = bid % BH;
-  const int bb = bh / H, hh = bh - bb * H;
-  const T* Q = static_cast<const T*>(Qv) + bb * qs.b + hh * qs.h;
-  const T* K = static_cast<const T*>(Kv) + bb * ks.b + hh * ks.h;
-  const T* V = static_cast<const T*>(Vv) + bb * vs.b + hh * vs.h;
-  const int q_row_bytes = (int)qs.n * 2;
+  const int bb = kDense ? 0 : bh / H, hh = kDense ? 0 : bh - bb * H;
+  const long long dense_head = (long long)bh * Nq * Sh::kD;
+  const T* Q = static_cast<const T*>(Qv) + (kDense ? dense_head : bb * qs.b + hh * qs.h);
+  const T* K = static_cast<const T*>(Kv) + (kDense ? dense_head : bb * ks.b + hh * ks.h);
+  const T* V = static_cast<const T*>(Vv) + (kDense ? dense_head : bb * vs.b + hh * vs.h);
+  const int q_row_bytes = kDense ? Sh::kD * 2 : (int)qs.n * 2;
   const int q0 = rb * kWaveRows;
   const int qrow = q0 + r32;
 
   StepArgs a;
-  a.k_row_bytes = (int)ks.n * 2;
-  a.v_row_bytes = (int)vs.n * 2;
+  a.k_row_bytes = kDense ? Sh::kD * 2 : (int)ks.n * 2;
+  a.v_row_bytes = kDense ? Sh::kD * 2 : (int)vs.n * 2;
   a.k_rsrc = head_desc(K, Nk, a.k_row_bytes);
   a.v_rsrc = head_desc(V, Nk, a.v_row_bytes);
   a.d_chunks = D >> 3;
@@ -1181,6 +1194,8 @@ __global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_ker
   }
   if (a.nAct > 0) issue_split_half<Sh>(a, wring, wave);
   if (a.nAct > 1) issue_split_half<Sh>(a, wring + L::kSlotBytes, wave + L::kWaves);
+  // The LSE pointer is not preloaded: load it while the halves are in flight, not at the store.
+  if constexpr (Sh::kLse) asm volatile("" ::"s"(LSE));
 
   WaveState<Sh> w;
 #pragma unroll
@@ -1277,7 +1292,8 @@ __global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_ker
   // in store_o).
   constexpr int kC8 = Sh::kD / 8;
   constexpr int kItems = L::kRowsPerWave * kC8;
-  T* O = static_cast<T*>(Ov) + bb * os.b + hh * os.h;
+  T* O = static_cast<T*>(Ov) + (kDense ? dense_head : bb * os.b + hh * os.h);
+  const long long o_rs = kDense ? (long long)Sh::kD : os.n;
 #pragma unroll
   for (int pass = 0; pass < (kItems + 63) / 64; ++pass) {
     const int item = 64 * pass + lane_e;
@@ -1311,7 +1327,7 @@ __global__ __launch_bounds__(SplitLayout<Sh>::kWaves * 64, 1) void fwd_split_ker
     }
     const int qr = q0 + R;
     if (qr < Nq && (!Sh::kMaskD || c8 < a.d_chunks)) {
-      u32x4* dst = reinterpret_cast<u32x4*>(O + (long long)qr * os.n + 8 * c8);
+      u32x4* dst = reinterpret_cast<u32x4*>(O + (long long)qr * o_rs + 8 * c8);
       if constexpr (Sh::kMaskD)
         *dst = __builtin_bit_cast(u32x4, ov);
       else
@@ -1439,21 +1455,31 @@ struct LaunchArgs {
 template <class Sh, bool kDense>
 static void launch_instance(const LaunchArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((fwd_kernel<Sh, kDense>), dim3(a.BH * a.nQB), dim3(kThreads), 0, stream, a.q,
-                     a.k, a.v, a.o, a.lse, a.H, a.BH, a.Nq, a.Nk, a.D, a.nQB, a.scale_log2,
-                     a.causal, a.qs, a.ks, a.vs, a.os);
+                     a.k, a.v, a.o, a.BH, a.Nq, a.Nk, a.nQB, a.causal, a.scale_log2, a.lse, a.H,
+                     a.D, a.qs, a.ks, a.vs, a.os);
 }
 
-template <class Sh>
+template <class Sh, bool kDense = false>
 static void launch_split_instance(const LaunchArgs& a, hipStream_t stream) {
   const int nRB = (a.Nq + kWaveRows - 1) / kWaveRows;
-  hipLaunchKernelGGL((fwd_split_kernel<Sh>), dim3(a.BH * nRB), dim3(SplitLayout<Sh>::kWaves * 64), 0, stream, a.q,
-                     a.k, a.v, a.o, a.lse, a.H, a.BH, a.Nq, a.Nk, a.D, nRB, a.scale_log2,
-                     a.causal, a.qs, a.ks, a.vs, a.os);
+  hipLaunchKernelGGL((fwd_split_kernel<Sh, kDense>), dim3(a.BH * nRB),
+                     dim3(SplitLayout<Sh>::kWaves * 64), 0, stream, a.q, a.k, a.v, a.o, a.BH,
+                     a.Nq, a.Nk, nRB, a.causal, a.scale_log2, a.lse, a.H, a.D, a.qs, a.ks, a.vs,
+                     a.os);
 }
 
 template <int kD, typename T>
 static void launch_dims(const LaunchArgs& a, bool dense, bool split, hipStream_t stream) {
   if (split) {
+    if constexpr (kD == 64 && std::is_same<T, __bf16>::value) {
+      if (dense && a.D == kD) {  // the reference's layout: no stride arguments to load
+        if (a.lse != nullptr)
+          launch_split_instance<Shape<kD, T, false>, true>(a, stream);
+        else
+          launch_split_instance<Shape<kD, T, false, false>, true>(a, stream);
+        return;
+      }
+    }
     if (a.D != kD)
       launch_split_instance<Shape<kD, T, true>>(a, stream);
     else if (a.lse != nullptr)
