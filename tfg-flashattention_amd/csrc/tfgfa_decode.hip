@@ -429,16 +429,17 @@ __device__ __forceinline__ void merge_splits(const float* part, int bh, int S, i
 // offsets follow from bh; the stride arguments are not read.
 //
 // Argument order: the first 14 dwords are preloaded into SGPRs at wave launch
-// (-amdgpu-kernarg-preload-count).  They hold what a workgroup needs before its first cache
-// loads and its length load (the caches, cache_seqlens, the arrival words, the sizes) and the
-// scale, so a dense workgroup issues them with no scalar load from the argument segment first.
-// Measured per graph-replayed step against the earlier order (q and the strides first):
-// B1 H25 L1024 6.72 -> 5.92 us, B1 H16 L8192 9.80 (from 10.66), B8 H25 L1024 12.06 -> 11.19.
+// (-amdgpu-kernarg-preload-count).  They hold what a workgroup needs for its first cache, q and
+// length loads (the caches, cache_seqlens, q, the sizes) and the scale, so a dense workgroup
+// issues them with no scalar load from the argument segment first; the other pointers are
+// loaded while those are in flight.  Measured per graph-replayed step against the earlier order
+// (q and the strides first, q loaded after the length): B1 H25 L1024 6.72 -> 5.90 us,
+// B1 H16 L8192 10.66 -> 9.66 us, B8 H25 L1024 12.06 -> 11.12 us.
 template <class Sh, int kW, bool kDense>
 __global__ __launch_bounds__(64 * kW) void decode_kernel(
     typename Sh::T* Kc, typename Sh::T* Vc, const int* __restrict__ seqlens,
-    u64* __restrict__ arrive, int N_max, int S, int C, int H, float scale_log2, int D,
-    const typename Sh::T* __restrict__ Q, u64 tag, typename Sh::T* __restrict__ O,
+    const typename Sh::T* __restrict__ Q, int N_max, int S, int C, int H, float scale_log2,
+    int D, u64* __restrict__ arrive, u64 tag, typename Sh::T* __restrict__ O,
     float* __restrict__ LSE, float* __restrict__ part, Vecs qs, Rows ks, Rows vs,
     const typename Sh::T* __restrict__ Kn, Vecs kns, const typename Sh::T* __restrict__ Vn,
     Vecs vns, Vecs os) {
@@ -484,15 +485,6 @@ __global__ __launch_bounds__(64 * kW) void decode_kernel(
   const int v_lane = g * vrow + 16 * c;
   const int c0 = s * C;
   int kb = c0 + wave * kWaveKeys;  // this wave's first block
-  // S > 1: this head's arrival word, read by wave 0 ahead of its cache loads.
-  u64* const aw = kSplit ? reinterpret_cast<u64*>(reinterpret_cast<char*>(arrive) +
-                                                  (long long)bh * kArriveStride)
-                         : nullptr;
-  u64 aw_start = 0;
-  if (kSplit) {
-    if (wave == 0) aw_start = __hip_atomic_load(aw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_sched_barrier(0);
-  }
   // The first block's loads go out before the cache length arrives from memory: over the whole
   // allocation (N_max rows, all addressable), with the rows at or past the length zeroed once
   // it is known (below), so no stale or appended-row value reaches the sums.
@@ -501,7 +493,30 @@ __global__ __launch_bounds__(64 * kW) void decode_kernel(
     load_block<Sh>(A, rows_rsrc(Kh, N_max * krow), rows_rsrc(Vh, N_max * vrow), krow, vrow, kb,
                    true, k_lane, v_lane, pmask);
 
+  // q does not depend on the cache length: its loads go out before the length is read.
+  uint32_t qp[4 * kDP];  // this lane's q pieces as element pairs (zero past the head dim)
+  {
+    const T* qh = Q + (kDense ? hvec : b * qs.b + h * qs.h);
+#pragma unroll
+    for (int p = 0; p < kDP; ++p) {
+      u32x4 qv = {0, 0, 0, 0};
+      if ((pmask >> p) & 1u) qv = *reinterpret_cast<const u32x4*>(qh + 32 * p + 8 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qp[4 * p + i] = qv[i];
+    }
+  }
+
   const int Lc = seqlens ? seqlens[b] : N_max;  // valid cached rows
+  // S > 1: this head's arrival word, read by wave 0 after its first cache, q and length loads
+  // are issued (it is needed after the cache loop).
+  u64* const aw = kSplit ? reinterpret_cast<u64*>(reinterpret_cast<char*>(arrive) +
+                                                  (long long)bh * kArriveStride)
+                         : nullptr;
+  u64 aw_start = 0;
+  if (kSplit) {
+    if (wave == 0) aw_start = __hip_atomic_load(aw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   const bool valid = Lc >= 0 && Lc + (append ? 1 : 0) <= N_max;
   const int L = valid ? Lc + (append ? 1 : 0) : 0;  // keys attended
   const int c1 = min(c0 + C, L);
@@ -510,7 +525,7 @@ __global__ __launch_bounds__(64 * kW) void decode_kernel(
   const __amdgpu_buffer_rsrc_t vd = rows_rsrc(Vh, Lr * vrow);
   // Arguments past the preloaded ones, needed once the first block is in: their loads go out
   // with the first block and the length rather than where they are used.
-  asm volatile("" ::"s"(Q), "s"(O), "s"(LSE), "s"(part), "s"(tag));
+  asm volatile("" ::"s"(O), "s"(LSE), "s"(part), "s"(tag));
 
   // The new token: stored into the cache by the workgroup whose chunk holds row Lc.
   u32x4 k_app[kDP], v_app[kDP];
@@ -536,18 +551,6 @@ __global__ __launch_bounds__(64 * kW) void decode_kernel(
           *reinterpret_cast<u32x4*>(Kh + (long long)Lc * ksn + 32 * p + 8 * c) = k_app[p];
           *reinterpret_cast<u32x4*>(Vh + (long long)Lc * vsn + 32 * p + 8 * c) = v_app[p];
         }
-    }
-  }
-
-  uint32_t qp[4 * kDP];  // this lane's q pieces as element pairs (zero past the head dim)
-  {
-    const T* qh = Q + (kDense ? hvec : b * qs.b + h * qs.h);
-#pragma unroll
-    for (int p = 0; p < kDP; ++p) {
-      u32x4 qv = {0, 0, 0, 0};
-      if ((pmask >> p) & 1u) qv = *reinterpret_cast<const u32x4*>(qh + 32 * p + 8 * c);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) qp[4 * p + i] = qv[i];
     }
   }
 
@@ -932,7 +935,7 @@ static int decode_step(const void* q, const int64_t* q_strides, void* k_cache,
                      (!append || (vecs_dense(kns, B, H, D) && vecs_dense(vns, B, H, D)));
 #define TFGFA_DECODE_LAUNCH_W(kDP, kMask, kW, kDn)                                            \
   hipLaunchKernelGGL((decode_kernel<DShape<T, kDP, kMask>, kW, kDn>), grid, dim3(64 * kW), 0, \
-                     stream, kc, vc, cache_seqlens, arrive, N_max, S, C, H, scale_log2, D, qt, \
+                     stream, kc, vc, cache_seqlens, qt, N_max, S, C, H, scale_log2, D, arrive, \
                      tag, ot, lse, ws, qs, ks, vs, knt, kns, vnt, vns, os)
 #define TFGFA_DECODE_LAUNCH(kDP, kMask, kDn)                 \
   do {                                                       \
