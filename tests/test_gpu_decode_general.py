@@ -11,7 +11,9 @@ the fused append (cache row written, nothing else touched), the split-sequence p
 the one-workgroup path, strided caches (bitwise equal to contiguous ones), NaN rows for
 invalid lengths, NaN / inf in cache rows past the length (no effect); and bf16 / D = 64
 bitwise equal to the bf16 entry point.  At D = 96 and 128, both sides of the split threshold
-(B*H at half the CUs splits, one head more does not).
+(B*H at half the CUs splits, one head more does not).  The dense instances (contiguous operands
+at D = 64 and 128, no strides read) bitwise equal to the strided ones, split and unsplit, with
+and without the append.
 """
 import sys
 
@@ -167,6 +169,44 @@ def test_strided_cache_is_bitwise_equal(dt, D):
     torch.cuda.synchronize()
     assert torch.equal(got[0].view(torch.int16), ref[0].view(torch.int16))
     assert torch.equal(got[1], ref[1])
+
+
+@pytest.mark.parametrize("append", [False, True])
+@pytest.mark.parametrize("B,H,N_max,lens", [(1, 4, 4096, [3000]), (8, 25, 256, [255, 7, 128, 0, 200, 31, 254, 100])])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dt", list(DTYPES))
+def test_dense_instances_equal_strided_ones(dt, D, B, H, N_max, lens, append):
+    """Every operand contiguous at D = 64 or 128 (the KVCache layout) takes the dense instances,
+    which compute offsets from the head index and read no strides; the same values in
+    (B, N_max, H, D) caches, with q, k_new, v_new and o as views of wider rows, take the strided
+    ones.  Results, and the appended cache row, must be bitwise equal: split heads (B*H = 4) and
+    one workgroup per head (B*H = 200)."""
+    _say(f"decode dense vs strided {dt} D={D} B={B} H={H} N_max={N_max} append={append}")
+    q, kc, vc = _case(B, H, N_max, D, 300 + D + B, dt)
+    kn, vn = _rand((B, H, D), 310 + D, dt, 3.0), _rand((B, H, D), 320 + D, dt)
+    lens = lens if not append else [min(L, N_max - 1) for L in lens]
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    kd, vd = _dev(kc, dt), _dev(vc, dt)
+    new = (_dev(kn, dt), _dev(vn, dt)) if append else (None, None)
+    ref = custom_flash_attn.decode(_dev(q, dt), kd, vd, sl, *new, return_lse=True)
+    ks = _dev(kc, dt).transpose(1, 2).contiguous().transpose(1, 2)
+    vs = _dev(vc, dt).transpose(1, 2).contiguous().transpose(1, 2)
+
+    def wide(x):  # (B, H, D) values as a view of (B, H, D + 8) rows
+        buf = torch.zeros(B, H, D + 8, dtype=DTYPES[dt], device=DEV)
+        buf[..., :D].copy_(x)
+        return buf[..., :D]
+
+    qv = wide(_dev(q, dt))
+    newv = (wide(new[0]), wide(new[1])) if append else (None, None)
+    ov = wide(torch.zeros(B, H, D, dtype=DTYPES[dt], device=DEV))
+    got = custom_flash_attn.decode(qv, ks, vs, sl, *newv, out=ov, return_lse=True)
+    torch.cuda.synchronize()
+    assert not qv.is_contiguous() and not ks.is_contiguous()
+    assert torch.equal(got[0].view(torch.int16), ref[0].view(torch.int16)), "O differs"
+    assert torch.equal(got[1], ref[1]), "LSE differs"
+    assert torch.equal(ks.view(torch.int16), kd.view(torch.int16)), "k caches differ"
+    assert torch.equal(vs.view(torch.int16), vd.view(torch.int16)), "v caches differ"
 
 
 @pytest.mark.parametrize("D", [8, 128])
