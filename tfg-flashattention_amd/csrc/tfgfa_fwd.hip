@@ -248,8 +248,9 @@ struct Shape {
   // K ring slots.  2: K_{j+2} is issued after tile step j's barrier, into the slot of K_j (last
   // read by half-step 2j, before the barrier), and has two half-steps to land.  3: K_{j+2} is
   // issued at the start of step j, into the slot of K_{j-1}, and has three.  Head dim 64 uses 2
-  // (as fast, measured, and it leaves LDS for the Q stage); head dim 128 uses 3 (2 was ~3%
-  // slower there).
+  // (as fast, measured, and it leaves LDS for the Q stage); head dim 128 uses 3: 2 slots (a third
+  // of the code, 64 KiB of LDS) measured 0.3-2.4% slower at d = 128, 120, 112, 72 and 96 (B1 H16
+  // N8192), faster only at B8 H25 N1024 d = 96 (2.7%).
   static constexpr int kKSlots = kD_ == 128 ? 3 : 2;
   // V ring: 2 slots; V_{j+1} is issued after step j's barrier, into the slot of V_{j-1} (read by
   // half-step 2j, before the barrier).
