@@ -1,7 +1,8 @@
 """The C ABI called directly through ctypes, as a non-Python FFI would bind it (GPU box only).
 
-Each compute entry point of include/tfgfa.h is called with the argument lists of the ctypes
-stubs in INTEGRATION.md, on raw device pointers from torch tensors.  Results are checked
+Each compute entry point of include/tfgfa.h is called with the argument lists a reference-side
+ctypes binding would use (argtypes from the header's prototypes), on raw device pointers from
+torch tensors.  Results are checked
 against the fp64 oracle (``attention_np``, ``decode_np``, pinned in tests/test_oracle.py) to
 the forward's tolerances (max|dO| <= 2e-2, mean|dO| <= 2e-3, max|dLSE| <= 1e-3) and bitwise
 against the Python package, which reaches the same library through pybind11.
@@ -136,7 +137,8 @@ def _decode_case(B, H, N_max, D, dtype, seed):
 
 @pytest.mark.parametrize("dtype,dcode,D", [(torch.bfloat16, 0, 64), (torch.float16, 1, 96)])
 def test_decode_ctypes_stub_appends_and_attends(lib, dtype, dcode, D):
-    """The INTEGRATION.md decode stub: append at cache_seqlens, attend, advance the lengths."""
+    """A ctypes decode loop as a reference-side caller would write it: append at cache_seqlens,
+    attend, advance the lengths."""
     B, H, N_max, lens = 2, 4, 2048, [1500, 7]
     q, kc, vc, kn, vn = _decode_case(B, H, N_max, D, dtype, 20 + D)
     k_ref, v_ref = _np(kc), _np(vc)
