@@ -115,6 +115,21 @@ def test_decode_noalloc_scratch_holds_the_split_on_256_cus(lib):
     assert lib.tfgfa_decode_splits(1, 4, 8192, 64, 256, 0) == 1  # no workspace: no split
 
 
+def test_stream_read_validates_before_any_hip_call(lib):
+    """tfgfa_stream_read (the measurement floor of the split decode legs) checks its arguments
+    on the host: nothing to read is a no-op, a null pointer or a misaligned pointer or size is
+    an error, all without touching a device."""
+    lib.tfgfa_stream_read.restype = ctypes.c_int
+    lib.tfgfa_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    P, S = 0x10000, 0x20000  # never dereferenced: every call below returns before a launch
+    assert lib.tfgfa_stream_read(P, 0, S, None) == _header_define("TFGFA_OK")
+    assert lib.tfgfa_stream_read(None, 4096, S, None) == _header_define("TFGFA_ERR_NULL_POINTER")
+    assert lib.tfgfa_stream_read(P, 4096, None, None) == _header_define("TFGFA_ERR_NULL_POINTER")
+    assert lib.tfgfa_stream_read(P + 8, 4096, S, None) == _header_define("TFGFA_ERR_ALIGNMENT")
+    assert lib.tfgfa_stream_read(P, 4100, S, None) == _header_define("TFGFA_ERR_ALIGNMENT")
+    assert lib.tfgfa_stream_read(P, 4096, S + 2, None) == _header_define("TFGFA_ERR_ALIGNMENT")
+
+
 def test_abi_version(lib):
     assert lib.tfgfa_abi_version() == _header_define("TFGFA_ABI_VERSION")
     assert _C.abi_version() == _header_define("TFGFA_ABI_VERSION")
