@@ -311,10 +311,36 @@ def time_generate(dev, runs=5, warmup=2):
     return out
 
 
+def _per_call_ms_pair(step_a, step_b, stream, calls=MIN_PER_CALL, group=10):
+    """_per_call_ms for two workloads timed in alternating groups of ``group`` launches (a, b, a,
+    b, ...), so that both see the same clocks; (median, mean) of each."""
+    import torch
+
+    ngroups = max(1, calls // group)
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(ngroups)] for _ in range(2)]
+    torch.cuda.synchronize()
+    for gi in range(ngroups):
+        for which, step in ((0, step_a), (1, step_b)):
+            a, b = ev[which][gi]
+            a.record(stream)
+            for j in range(group):
+                step(gi * group + j)
+            b.record(stream)
+    torch.cuda.synchronize()
+    out = []
+    for which in range(2):
+        ms = [a.elapsed_time(b) / group for a, b in ev[which]]
+        out.append((statistics.median(ms), statistics.fmean(ms)))
+    return out
+
+
 def time_strided_views(dev, steps=MIN_PER_CALL):
     """Same workload through tfgfa_fwd_bf16_strided with the operands of a GPT-2 block as they
     come out of the Q/K/V projections: (B, N, H, 64) buffers read as (B, H, N, 64) views and O
-    written into a (B, N, H, 64) buffer (no copies before or after the kernel)."""
+    written into a (B, N, H, 64) buffer (no copies before or after the kernel).  Timed in
+    alternating groups with the dense O + LSE launch over the same values (contiguous copies),
+    so the strided/dense ratio is not a difference of clocks between two legs."""
     import torch
 
     from custom_flash_attn import _C
@@ -322,25 +348,38 @@ def time_strided_views(dev, steps=MIN_PER_CALL):
     gen = torch.Generator(device=dev).manual_seed(2003)
     sets = []
     for _ in range(N_SETS):
-        q, k, v = ((torch.randn(B, N, H, D, device=dev, generator=gen) * s).to(torch.bfloat16).transpose(1, 2)
-                   for s in (SIGMA_QK, SIGMA_QK, SIGMA_V))
+        qd, kd, vd = ((torch.randn(B, H, N, D, device=dev, generator=gen) * s).to(torch.bfloat16)
+                      for s in (SIGMA_QK, SIGMA_QK, SIGMA_V))
+        q, k, v = (x.transpose(1, 2).contiguous().transpose(1, 2) for x in (qd, kd, vd))
         o = torch.empty(B, N, H, D, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+        od = torch.empty_like(qd)
         lse = torch.empty(B, H, N, device=dev, dtype=torch.float32)
-        sets.append((q, k, v, o, lse))
+        sets.append((q, k, v, o, qd, kd, vd, od, lse))
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
 
     def step(i):
-        q, k, v, o, lse = sets[i % N_SETS]
+        q, k, v, o, _, _, _, _, lse = sets[i % N_SETS]
         _C.fwd_strided(q.data_ptr(), q.stride(), k.data_ptr(), k.stride(), v.data_ptr(), v.stride(),
                        o.data_ptr(), o.stride(), lse.data_ptr(), B, H, N, D, SCALE, True, sh)
 
+    def step_dense(i):
+        _, _, _, _, qd, kd, vd, od, lse = sets[i % N_SETS]
+        _C.fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), od.data_ptr(), lse.data_ptr(),
+               B, H, N, D, SCALE, True, sh)
+
     _warm(step)
-    med, mean = _per_call_ms(step, stream, max(steps, MIN_PER_CALL))
+    _warm(step_dense)
+    calls = max(steps, MIN_PER_CALL)
+    (med, mean), (med_d, mean_d) = _per_call_ms_pair(step, step_dense, stream, calls)
     return {"layout": "q, k, v: (B, N, H, 64) buffers viewed (B, H, N, 64); o: (B, N, H, 64) buffer",
             "ms_per_call_median": round(med, 5), "ms_per_call_mean": round(mean, 5),
             "value": round(flops_per_fwd() / (med * 1e-3) / 1e12, 2),
-            "unit": "TFLOP/s", "calls": max(steps, MIN_PER_CALL)}
+            "unit": "TFLOP/s", "calls": calls,
+            "dense_ms_per_call_median": round(med_d, 5),
+            "strided_over_dense": round(med / med_d, 4),
+            "timing": "groups of 10 launches alternating with the dense O + LSE launch over the "
+                      "same values (contiguous copies), both with the LSE"}
 
 
 DEC_SETS = 6  # 6 x 52 MB of K/V cache: more than the 256 MB Infinity Cache
