@@ -382,6 +382,37 @@ def time_strided_views(dev, steps=MIN_PER_CALL):
                       "same values (contiguous copies), both with the LSE"}
 
 
+def time_torch_sdpa(dev, steps=MIN_PER_CALL):
+    """For context only: PyTorch's own fused causal attention (F.scaled_dot_product_attention
+    restricted to its flash backend; the math fallback is not allowed) on the headline workload,
+    same inputs and timing as the per-call legs.  Reported beside the headline, never as it."""
+    import torch
+    import torch.nn.functional as F
+
+    gen = torch.Generator(device=dev).manual_seed(1003)
+    sets = []
+    for _ in range(N_SETS):
+        sets.append(tuple((torch.randn(B, H, N, D, device=dev, generator=gen) * s).to(torch.bfloat16)
+                          for s in (SIGMA_QK, SIGMA_QK, SIGMA_V)))
+    stream = torch.cuda.current_stream(dev)
+    try:
+        backend = torch.nn.attention.SDPBackend.FLASH_ATTENTION
+        with torch.nn.attention.sdpa_kernel(backend):
+            def step(i):
+                q, k, v = sets[i % N_SETS]
+                F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=SCALE)
+
+            _warm(step)
+            med, mean = _per_call_ms(step, stream, max(steps, MIN_PER_CALL))
+    except Exception as e:  # a build of torch without the fused backend: say so
+        return {"unavailable": f"{type(e).__name__}: {str(e)[:200]}"}
+    return {"call": "torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True), "
+                    "SDPBackend.FLASH_ATTENTION only, torch " + torch.__version__,
+            "ms_per_call_median": round(med, 5), "ms_per_call_mean": round(mean, 5),
+            "value": round(flops_per_fwd() / (med * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+            "role": "context: the framework's fused attention on the same box and workload"}
+
+
 DEC_SETS = 6  # 6 x 52 MB of K/V cache: more than the 256 MB Infinity Cache
 
 
@@ -843,6 +874,8 @@ def main():
                     help="skip the decode-step leg (KV-cache attention, HBM-bound)")
     ap.add_argument("--no-generate", action="store_true",
                     help="skip the token-generation leg (the reference's generate() benchmark)")
+    ap.add_argument("--no-torch-sdpa", action="store_true",
+                    help="skip the context leg timing torch's own fused causal attention")
     ap.add_argument("--no-strided", action="store_true",
                     help="skip the second timing of the same workload on strided (B, N, H, 64) views")
     ap.add_argument("--no-surface", action="store_true",
@@ -1015,6 +1048,8 @@ def main():
         result["triton_wrapper_surface"] = time_surface(dev)
     if not args.no_strided:
         result["strided_gpt2_views"] = time_strided_views(dev)
+    if not args.no_torch_sdpa:
+        result["torch_sdpa_same_box"] = time_torch_sdpa(dev)
     if not args.no_decode:
         result["decode"] = time_decode(dev)
         result["decode_split"] = time_decode_split(dev)
