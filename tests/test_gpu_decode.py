@@ -72,6 +72,10 @@ def _case(B, H, N_max, seed):
     (4, 2, 257, [129, 256, 2, 257]),
     (1, 16, 8192, [8192]),
     (2, 3, 5000, [4097, 3]),
+    # 2048 heads, one workgroup each over many dispatch rounds, ragged lengths
+    (64, 32, 300, [1 + (37 * b) % 300 for b in range(64)]),
+    # 133 heads: just above half the CUs (not split), not a multiple of the 8 XCDs
+    (7, 19, 1500, [1500, 1, 749, 1024, 3, 1499, 777]),
 ])
 def test_decode_matches_oracle(B, H, N_max, lens):
     _say(f"decode B={B} H={H} N_max={N_max} lens={lens}")

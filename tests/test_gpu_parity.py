@@ -183,6 +183,30 @@ def test_config_every_row_vs_fp64_oracle(name):
     _check(o, lse, o_ref, lse_ref, f"{name} every row")
 
 
+@pytest.mark.parametrize("B,H,N,nheads", [
+    (32, 128, 256, 48),   # 4096 heads, 8192 workgroups: many dispatch rounds
+    (3, 37, 1000, 24),    # 111 heads, not a multiple of the 8 XCDs; ragged last block
+    (5, 13, 129, 0),      # 65 heads, a one-row last block (split-key kernel)
+    (1, 3, 777, 0),       # 3 heads (split-key kernel), ragged
+])
+def test_grid_shapes_many_and_odd_head_counts(B, H, N, nheads):
+    """Grids the configs do not cover: thousands of heads, head counts that do not divide
+    over the XCDs (a head's blocks then land on different XCDs), one-row and ragged last
+    blocks.  O and LSE of every row of nheads sampled heads (0: all heads) against the fp64
+    oracle."""
+    q, k, v = (_bf(_rand((B, H, N, 64), 7000 + B * H + N + i, 2.0 if i < 2 else 1.0)) for i in range(3))
+    _say(f"grid B={B} H={H} N={N}")
+    o, lse = _run(q, k, v)
+    if nheads:
+        g = np.random.Generator(np.random.PCG64(B * H + N))
+        idx = np.unique(np.concatenate([[0, B * H - 1], g.choice(B * H, nheads, replace=False)]))
+    else:
+        idx = np.arange(B * H)
+    pick = lambda x: np.ascontiguousarray(x.reshape(B * H, N, -1)[idx][None])
+    o_ref, lse_ref = attention_c(pick(q), pick(k), pick(v), 0.125, True)
+    _check(pick(o), lse.reshape(B * H, N)[idx][None], o_ref, lse_ref, f"B={B} H={H} N={N}")
+
+
 # ------------------------------------------------------------------ reference test shapes
 
 
