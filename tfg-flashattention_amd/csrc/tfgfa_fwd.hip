@@ -153,11 +153,18 @@ struct Elem<_Float16> {
   static __device__ __forceinline__ f32x16 mfma(v8 a, v8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  // P <= 2^15 stays inside fp16's range (65504).
+  // Offset margin of the lane-max check of a wave's last half: P <= 2^15 stays inside fp16's
+  // range (65504).
   static constexpr float kMargin = 15.0f;
-  // What a sum check would need (every rounded P finite in fp16); the fp16 instances use the
-  // lane-max check instead, which moves the offset less often at this bound.
-  static constexpr float kSumBound = 65504.0f;
+  // Bound of the fused half-step's sum check: the largest finite float.  The conversion to fp16
+  // gives +inf for a P above fp16's range, so the rounded sum exceeds the bound (is +inf or a
+  // NaN) exactly when some rounded P is not finite; every finite one is at most 65504, which
+  // keeps l_p and |O| / max|V| below 2^16 times the number of keys.  Measured against checking
+  // the lane max of the scores against the margin on every half-step (the rounded sum is
+  // computed anyway, the lane max is ~10 more VALU instructions), interleaved, µs: B1 H16 N8192
+  // 171.7 -> 165.9, B8 H16 N1024 d = 128 54.7 -> 54.0, B8 H25 N1024 (sigma = 3, O + LSE)
+  // 50.2 -> 49.6.
+  static constexpr float kSumBound = 0x1.fffffep127f;
   static __device__ __forceinline__ float sum8(v8 p, float acc) {
     typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
     const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
@@ -538,15 +545,15 @@ __device__ __forceinline__ typename Elem<typename Sh::T>::v8 k_operand(const Wav
 //                    P_u = exp2(scale*log2e*S_u - m_run)
 //   chunks kPv+1..   MFMA i of S_{u+1} = K_{u+1} Q^T, the next operand read, a share of
 //                    the sums of P_u and its conversion to the element type
-// The offset check (bf16) reads the lane's running sum l_p with this half's probabilities, as
-// rounded to the element type, added: a rounded P above 2^64 makes that sum exceed it (an
+// The offset check reads the lane's running sum l_p with this half's probabilities, as rounded
+// to the element type, added.  bf16: a rounded P above 2^64 makes that sum exceed the bound (an
 // overflow gives +inf, a -inf offset on a wave's first half gives +inf or NaN), so a sum above
 // the bound, or not a number, takes the rare branch: move the offset to the rows' exact running
 // max, rescale O and the sums, recompute P_u.  A sum above the bound without any single P above
 // it moves the offset early, which is harmless (after a move every P is at most 1, so l_p stays
 // below the number of keys).  So l_p, and with it every P and |O| / max|V|, stays at most 2^64.
-// fp16 checks the lane max of the scores against the margin instead, in chunk 0, and takes the
-// same branch.
+// fp16: the bound is the largest finite float, exceeded exactly when a rounded P is +inf (above
+// fp16's range) or a NaN, so every P that reaches an MFMA is finite.
 template <class Sh, int kVs, int kVh, int kKs, int kKh, bool kPV = true>
 __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, float scale_log2,
                                            float inv_scale_log2) {
@@ -559,15 +566,6 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
   if constexpr (kPV) {
     vop[0] = v_operand<Sh, kVs, kVh>(w, lds, 0);
     vop[1] = v_operand<Sh, kVs, kVh>(w, lds, 1);
-  }
-  // fp16 keeps the lane-max check (a score more than the margin above the offset): its sum
-  // bound is tight enough that the sum check moved the offset more often.
-  constexpr bool kMaxCheck = std::is_same<T, _Float16>::value;
-  float mx = 0.f;
-  bool max_move = false;
-  if constexpr (kMaxCheck) {
-    mx = lane_max(w);
-    max_move = __builtin_amdgcn_ballot_w64(mx > w.thr) != 0;
   }
   TFGFA_FENCE();
   const float neg_m = -w.m_run;
@@ -612,16 +610,13 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
       convert(p);
       asm volatile("" : "+v"(w.pb[0]), "+v"(w.pb[1]));
     } else if (i == 1) {
-      // bf16: the running sum with this half's rounded probabilities added (one of the two
-      // dot2 chains starts from l_p); fp16: the half's own sum.
-      const float l_old = w.l_p;
-      float hs = Elem<T>::sum8(w.pb[0], kMaxCheck ? 0.f : l_old) + Elem<T>::sum8(w.pb[1], 0.f);
+      // The running sum with this half's rounded probabilities added (one of the two dot2
+      // chains starts from l_p).
+      float hs = Elem<T>::sum8(w.pb[0], w.l_p) + Elem<T>::sum8(w.pb[1], 0.f);
       // As unsigned integers, the bits of a sum >= +0 exceed those of the bound exactly when
       // the sum does, is +inf or is a NaN (the device pass assumes no NaN in float compares).
-      const bool move = kMaxCheck ? max_move
-                        : __builtin_amdgcn_ballot_w64(__float_as_uint(hs) > __float_as_uint(kSumBound)) != 0;
-      if (move) {
-        if constexpr (!kMaxCheck) mx = lane_max(w);
+      if (__builtin_amdgcn_ballot_w64(__float_as_uint(hs) > __float_as_uint(kSumBound)) != 0) {
+        const float mx = lane_max(w);
         const float m_new = fmaxf(w.m_run, pair_max(mx) * scale_log2);
         const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
         w.m_run = m_new;
@@ -636,12 +631,9 @@ __device__ __forceinline__ void fused_step(WaveState<Sh>& w, const Lds& lds, flo
         for (int t = 0; t < 16; ++t) p[t] = __builtin_amdgcn_exp2f(fmaf(w.s[t], scale_log2, -m_new));
         convert(p);
         hs = Elem<T>::sum8(w.pb[0], 0.f) + Elem<T>::sum8(w.pb[1], 0.f);
-        if constexpr (!kMaxCheck) hs += w.l_p;  // l_p already rescaled by alpha
+        hs += w.l_p;  // l_p already rescaled by alpha
       }
-      if constexpr (kMaxCheck)
-        w.l_p += hs;
-      else
-        w.l_p = hs;
+      w.l_p = hs;
       asm volatile("" : "+v"(w.l_p));
     } else if (i == 2 && Sh::kLse) {
       float s0 = p[0], s1 = p[1];
