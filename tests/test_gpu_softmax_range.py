@@ -1,13 +1,14 @@
 """The forward's softmax over extreme score patterns (GPU box only).
 
-The kernel keeps a per-row exp2 offset that moves only when (bf16) a lane's running sum of its
-probabilities, as rounded for the MFMA, would pass 2^64, or (fp16, and a wave's last half) when
-a score passes it by a margin (60 log2 units for bf16, 15 for fp16); a move rescales O and both
-sums and recomputes the half's probabilities.  Random inputs at the configs' scales move it about
-once per row, so these cases force the other paths: scores that climb by far more than the
-margin every half (a move on every half, with rescale factors that underflow to 0), scores
-that fall (no move after the first half), halves that alternate high and low, and scores of
-magnitude ~1e4 (one-hot rows).
+The kernel keeps a per-row exp2 offset that moves only when a lane's running sum of its
+probabilities, as rounded for the MFMA, would pass a bound (bf16: 2^64; fp16: the largest finite
+float, passed exactly when a probability rounds to +inf, i.e. leaves fp16's range), or (a wave's
+last half) when a score passes it by a margin (60 log2 units for bf16, 15 for fp16); a move
+rescales O and both sums and recomputes the half's probabilities.  Random inputs at the configs'
+scales move it about once per row, so these cases force the other paths: scores that climb by
+far more than the margin every half (a move on every half, with rescale factors that underflow
+to 0), scores that fall (no move after the first half), halves that alternate high and low,
+scores of magnitude ~1e4 (one-hot rows), and probabilities at each element type's own bound.
 
 Oracle: attention_np (fp64, tests/test_oracle.py) on the same bf16/fp16-rounded inputs.
 Tolerances as everywhere: max|dO| <= 2e-2, mean|dO| <= 2e-3; LSE within 1e-3 plus the fp32
@@ -151,3 +152,36 @@ def test_bf16_range_past_bound_overflows_as_documented():
     finite_rows = np.isfinite(o).all(axis=-1)
     _say(f"range past bound: non-finite rows {int((~finite_rows).sum())} of {finite_rows.size}")
     assert not finite_rows[:, :, -1].any()
+
+
+@pytest.mark.parametrize("log2p", [15.9, 16.1])
+def test_f16_probabilities_at_the_edge_of_fp16(log2p):
+    """fp16 at its own bound: q = (16, 0, ...), k_j = 0 for j < 32 and (c, 0, ...) after, so every
+    later key scores log2p log2 units above the offset set by keys 0..31.  At 15.9 each rounded
+    probability (2^15.9 ~ 61147) is finite in fp16: no move, and the P.V of every later half runs
+    with those probabilities.  At 16.1 (2^16.1 ~ 70240 > 65504) the conversion gives +inf, the
+    rounded sum passes the bound and the offset moves.  Both must match the fp64 oracle with every
+    output finite, O-only bitwise equal to O + LSE."""
+    N, D = 1024, 64
+    c = torch.tensor(log2p * 8.0 / (16.0 * math.log2(math.e)), dtype=torch.float16).item()
+    q = np.zeros((1, 2, N, D), dtype=np.float32)
+    k = np.zeros((1, 2, N, D), dtype=np.float32)
+    q[..., 0] = 16.0
+    k[:, :, 32:, 0] = c
+    g = np.random.Generator(np.random.PCG64(int(log2p * 10)))
+    v = torch.from_numpy(g.standard_normal((1, 2, N, D), dtype=np.float32)).half().float().numpy()
+    qd, kd, vd = (torch.from_numpy(x).half().to(DEV) for x in (q, k, v))
+    o, lse = custom_flash_attn.attention(qd, kd, vd, return_lse=True)
+    o_only = custom_flash_attn.attention(qd, kd, vd)
+    torch.cuda.synchronize()
+    assert torch.equal(o_only.view(torch.int16), o.view(torch.int16)), "O-only call differs"
+    o_ref, l_ref = attention_np(q, k, v, 1.0 / math.sqrt(D), True)
+    o = o.float().cpu().numpy().astype(np.float64)
+    lse = lse.cpu().numpy().astype(np.float64)
+    d = np.abs(o - o_ref)
+    dl = np.abs(lse - l_ref)
+    _say(f"fp16 edge 2^{log2p}: c={c}; max|dO|={d.max():.3e} mean|dO|={d.mean():.3e} "
+         f"max|dLSE|={dl.max():.3e}")
+    assert np.isfinite(o).all() and np.isfinite(lse).all(), "non-finite output"
+    assert d.max() <= 2e-2 and d.mean() <= 2e-3
+    assert (dl <= 1e-3 + 4e-7 * np.abs(l_ref)).all()
