@@ -34,12 +34,13 @@
  * Scores and sums are fp32.  The softmax offset of a row moves lazily: only when the
  * probabilities taken against the current offset grow too large (bf16: a lane's running
  * sum of them would pass 2^64, or, in a wave's last 32-key half, a probability would pass
- * 2^60; fp16: a probability would pass 2^15) does it jump to the row's running maximum (the
+ * 2^60; fp16: a probability rounded to fp16 would be infinite, i.e. above 65504, or, in a
+ * wave's last half, would pass 2^15) does it jump to the row's running maximum (the
  * reference moves it on every tile, src/cpp/headers/v1_implementation.hpp:121-128).  So the
  * fp32 accumulators of P.V and of the sums stay finite while
  *     max|V| < 2^62          (bf16, any N_k; the reference's exact offset allows
  *                             N_k * max|V| < 2^128),
- *     N_k * max|V| < 2^113   (fp16; always true, fp16 values are below 2^16).
+ *     N_k * max|V| < 2^112   (fp16; always true, fp16 values are below 2^16).
  * Past that bound a bf16 row may come out inf or NaN where the exact-offset reference
  * stays finite.  LSE is not affected.
  */
